@@ -1,0 +1,251 @@
+"""Decode-step benchmark of the MI355X KV-cache hot path.
+
+Workload (the north-star shape): Llama-3-8B KV
+geometry (32 layers, 32 query / 8 KV heads, head_dim 128), f16 paged KV with
+32-token pages, batch 64, every sequence at context 8192.  One step = the
+decode step of the reference generator for every layer: append one token per
+sequence (K/V rows fp32 -> f16 into the paged pool) and split-K GQA attention
+over the 8193 cached tokens.  Pages are placed by a seeded random permutation
+of the pool (installed through the actor's free stack); cache contents are
+synthetic N(0,1) f16 written straight into the pool (the append kernel writes
+the step's new token); Q is N(0,1)/sqrt(128), the kernel scale 1/sqrt(128)
+(the reference always applies 1/sqrt(head_dim), detail.hpp:3163).
+
+Each timed step re-appends at position 8192 and attends over 8193 tokens, so
+every step does identical work.  `value` is KV-read GB/s: K+V bytes the
+attention must read per step / step time.  The roofline object covers the
+dominant kernel (split-K decode attention), timed with HIP events on the
+stream it runs on.  The CPU baseline is the oracle's restatement of the
+reference's paged decode route, timed on this host on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "emel.cpp_amd"))
+
+HBM_PEAK_GBS = 8000.0
+
+CONFIGS = {
+    # name: (n_layer, n_head, n_kv, head_dim, block_tokens, batch, ctx, kv_type)
+    "llama3-8b-b64-ctx8k": (32, 32, 8, 128, 32, 64, 8192, "f16"),
+    "llama3-8b-q8_0-b32-ctx16k": (32, 32, 8, 128, 32, 32, 16384, "q8_0"),
+    "llama3.2-1b-b16-ctx1k-4k": (16, 32, 8, 64, 16, 16, None, "f16"),
+    "qwen3-0.6b-b1-ctx512": (28, 16, 8, 128, 16, 1, 512, "f16"),
+}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="llama3-8b-b64-ctx8k", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--seed", type=int, default=1234)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only: the KV hot path shards by "
+                          "sequence with no exchange (see DESIGN.md); run with --gpus 1"}))
+        sys.exit(2)
+
+    import torch
+    import emelk
+
+    dev = torch.device("cuda:0")
+    L, H, HK, D, BT, B, CTX, kvt = CONFIGS[args.config]
+    kv_type = emelk.KV_F16 if kvt == "f16" else emelk.KV_Q8_0
+    rng = np.random.default_rng(args.seed)
+    if CTX is None:
+        ctx = rng.integers(1024, 4097, size=B).astype(np.int64)
+    else:
+        ctx = np.full(B, CTX, dtype=np.int64)
+    lens = ctx + 1  # tokens attended after the step's append
+    pages_per_seq = -(-lens // BT)
+    max_blocks = int(pages_per_seq.sum()) + 1
+    assert max_blocks <= emelk.MAX_BLOCKS
+
+    # ---- block map through the actor (seeded page permutation) ----
+    actor = emelk.KvActor()
+    ok, err = actor.reserve(B, max_blocks, BT)
+    assert ok, err
+    actor.set_free_order(rng.permutation(max_blocks).astype(np.uint16))
+    for s in range(B):
+        assert actor.allocate_sequence(s)[0]
+        assert actor.allocate_slots(s, int(ctx[s]))[0]
+    for s in range(B):
+        ok, err, _ = actor.allocate_slots(s, 1)  # the decode step's slot
+        assert ok, err
+    stride = int(pages_per_seq.max()) + 1
+    tables_h = actor.export_block_tables(list(range(B)), stride)
+    tables = torch.from_numpy(tables_h.view(np.int16)).to(dev)
+
+    g = emelk.geometry(L, H, HK, D, BT, max_blocks, kv_type)
+    pool_bytes = emelk.pool_bytes(g)
+    log(f"[bench] config={args.config} pools 2 x {pool_bytes / 1e9:.2f} GB, "
+        f"pages={max_blocks}")
+    k_pool = torch.empty(pool_bytes, dtype=torch.uint8, device=dev)
+    v_pool = torch.empty(pool_bytes, dtype=torch.uint8, device=dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    chunk = 1 << 30
+    t0 = time.time()
+    for pool in (k_pool, v_pool):
+        if kv_type == emelk.KV_F16:
+            h = pool.view(torch.float16)
+            for i in range(0, h.numel(), chunk):
+                n = min(chunk, h.numel() - i)
+                h[i:i + n].normal_(generator=gen)
+        else:
+            # q8_0 pages are written by quantizing N(0,1) rows (1% x20
+            # outliers) with the append kernel, one layer and page range at
+            # a time.
+            pass
+    if kv_type == emelk.KV_Q8_0:
+        for layer in range(L):
+            for s0 in range(0, B, 8):
+                s1 = min(B, s0 + 8)
+                n = int(ctx.max())
+                kr = torch.randn((s1 - s0, n, HK * D), generator=gen, device=dev)
+                vr = torch.randn((s1 - s0, n, HK * D), generator=gen, device=dev)
+                for t in (kr, vr):
+                    m = torch.rand(t.shape, generator=gen, device=dev) < 0.01
+                    t[m] *= 20.0
+                pos = torch.zeros(s1 - s0, dtype=torch.int32, device=dev)
+                emelk.append(g, k_pool, v_pool, layer, kr, vr, pos, tables[s0:s1])
+                del kr, vr
+    torch.cuda.synchronize()
+    log(f"[bench] pools filled in {time.time() - t0:.1f}s")
+
+    q = [(torch.randn((B, H, D), generator=gen, device=dev) / np.sqrt(D)).contiguous()
+         for _ in range(L)]
+    new_k = [torch.randn((B, 1, HK * D), generator=gen, device=dev) for _ in range(L)]
+    new_v = [torch.randn((B, 1, HK * D), generator=gen, device=dev) for _ in range(L)]
+    out = [torch.empty((B, H, D), dtype=torch.float32, device=dev) for _ in range(L)]
+    positions = torch.from_numpy(ctx.astype(np.int32)).to(dev)
+    kv_lens = torch.from_numpy(lens.astype(np.int32)).to(dev)
+    max_len = int(lens.max())
+    ws = torch.empty(emelk.decode_workspace_bytes(g, B, max_len) // 4 + 1, dtype=torch.float32,
+                     device=dev)
+    scale = float(1.0 / np.sqrt(D))
+    stream = torch.cuda.current_stream()
+
+    def step(events=None):
+        for layer in range(L):
+            emelk.append(g, k_pool, v_pool, layer, new_k[layer], new_v[layer], positions, tables)
+            if events is not None:
+                events[layer][0].record(stream)
+            emelk.decode(g, k_pool, v_pool, layer, q[layer], out[layer], kv_lens, max_len, tables,
+                         scale, ws)
+            if events is not None:
+                events[layer][1].record(stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    K = args.steps
+    ev = [[[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)]
+           for _ in range(L)] for _ in range(K)]
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    for k in range(K):
+        step(ev[k])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t_start
+    ms_per_step = 1e3 * elapsed / K
+    attn_ms = [e[0].elapsed_time(e[1]) for row in ev for e in row]
+    attn_avg_ms = float(np.mean(attn_ms))
+
+    # ---- algorithmic bytes ----
+    if kv_type == emelk.KV_F16:
+        row_bytes = HK * D * 2
+    else:
+        row_bytes = HK * (D + D // 32 * 2)
+    kv_read_layer = int(lens.sum()) * row_bytes * 2          # K and V rows attended
+    q_bytes = B * H * D * 4
+    o_bytes = B * H * D * 4
+    table_bytes = int(pages_per_seq.sum()) * 2
+    append_bytes = B * HK * D * 4 * 2 + B * row_bytes * 2
+    step_kv_bytes = kv_read_layer * L
+    step_bytes = (kv_read_layer + q_bytes + o_bytes + table_bytes + append_bytes) * L
+    kernel_bytes = kv_read_layer + q_bytes + o_bytes + table_bytes
+    kv_gbs = step_kv_bytes / (ms_per_step * 1e-3) / 1e9
+    achieved = kernel_bytes / (attn_avg_ms * 1e-3) / 1e9
+
+    # ---- full-size parity spot check on layer 0 + CPU baseline ----
+    parity = None
+    cpu = None
+    if not args.no_cpu_baseline and kv_type == emelk.KV_F16:
+        import oracle
+        nthreads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        layer = 0
+        lb = pool_bytes // L
+        kp = k_pool[layer * lb:(layer + 1) * lb].cpu().numpy().view(np.uint16)
+        vp = v_pool[layer * lb:(layer + 1) * lb].cpu().numpy().view(np.uint16)
+        # pool [page][kv_head][t][D] -> reference token-major [page*bt + t][kv_head*D]
+        kc = np.ascontiguousarray(kp.reshape(max_blocks, HK, BT, D).transpose(0, 2, 1, 3)
+                                  ).reshape(max_blocks * BT, HK * D)
+        vc = np.ascontiguousarray(vp.reshape(max_blocks, HK, BT, D).transpose(0, 2, 1, 3)
+                                  ).reshape(max_blocks * BT, HK * D)
+        del kp, vp
+        qh = q[layer].view(B, H * D).cpu().numpy()
+        want, secs = oracle.decode_batch_f16(qh, kc, vc, tables_h, lens, BT, H, HK, D,
+                                             int(lens.max()), scale, nthreads)
+        got = out[layer].view(B, H * D).cpu().numpy()
+        err = np.abs(got.astype(np.float64) - want)
+        within = bool(np.all(err <= 2e-3 + 1e-2 * np.abs(want)))
+        parity = {"layer": layer, "sequences": B, "max_abs_err": float(err.max()),
+                  "within_tolerance": within}
+        cpu_step_s = secs * L  # sample = 1 layer x all sequences; scaled to L layers
+        cpu = {"value": round(step_kv_bytes / cpu_step_s / 1e9, 4), "unit": "GB/s",
+               "cores": nthreads, "kind": "port",
+               "sample": f"1 layer x {B} sequences of the same step ({secs:.2f}s wall), "
+                         f"extrapolated x{L} layers; oracle restatement of compute_attention, "
+                         f"{nthreads} threads",
+               "steps_per_s": round(1.0 / cpu_step_s, 5)}
+
+    result = {
+        "metric": "KV-read HBM GB/s (% of peak) + decode steps/s, 8B-shape b64 ctx8k",
+        "value": round(kv_gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "steps_per_s": round(1e3 / ms_per_step, 3),
+        "pct_of_hbm_peak": round(100.0 * kv_gbs / HBM_PEAK_GBS, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16" if kv_type == emelk.KV_F16 else "q8_0",
+        "data": "synthetic (seeded N(0,1) K/V/Q, seeded random page permutation)",
+        "config": {"workload": args.config, "n_layer": L, "n_head": H, "n_head_kv": HK,
+                   "head_dim": D, "block_tokens": BT, "batch": B,
+                   "ctx": int(ctx[0]) if CTX else "U[1024,4096]", "kv": kvt,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "decode_kernel + combine_kernel (HIP events per layer call)",
+                     "bytes_per_launch": kernel_bytes, "avg_launch_ms": round(attn_avg_ms, 4)},
+        "cpu_baseline": cpu,
+        "parity_full_size": parity,
+    }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,82 @@
+// Shared device helpers for the gfx950 kernels (wave64, CDNA4).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace emelk::dev {
+
+typedef _Float16 half_t;
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t uint4_t __attribute__((ext_vector_type(4)));
+
+constexpr int k_wave = 64;
+
+// RNE fp32 -> f16 (v_cvt_f16_f32 under the default round-to-nearest-even mode).
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float v) {
+  const half_t h = static_cast<half_t>(v);
+  return __builtin_bit_cast(uint16_t, h);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
+  return static_cast<float>(__builtin_bit_cast(half_t, b));
+}
+
+__device__ __forceinline__ half2_t as_half2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
+__device__ __forceinline__ uint32_t as_u32(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
+
+// Packs two fp32 values into a half2 with RNE rounding.
+__device__ __forceinline__ half2_t pack_half2(float lo, float hi) {
+  half2_t r;
+  r.x = static_cast<half_t>(lo);
+  r.y = static_cast<half_t>(hi);
+  return r;
+}
+
+// fp32 += a.x*b.x + a.y*b.y  (v_dot2_f32_f16).
+__device__ __forceinline__ float dot2(half2_t a, half2_t b, float c) {
+  return __builtin_amdgcn_fdot2(a, b, c, false);
+}
+
+// DPP cross-lane moves inside 16-lane rows (gfx9 encodings).
+template <int ctrl>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), ctrl, 0xF, 0xF, false));
+}
+constexpr int k_dpp_quad_xor1 = 0xB1;  // quad_perm [1,0,3,2]
+constexpr int k_dpp_quad_xor2 = 0x4E;  // quad_perm [2,3,0,1]
+constexpr int k_dpp_row_half_mirror = 0x141;
+constexpr int k_dpp_row_mirror = 0x140;
+
+// Sum over aligned groups of `lanes` consecutive lanes (lanes in {2,4,8,16});
+// every lane of the group receives the group total.
+template <int lanes>
+__device__ __forceinline__ float group_sum(float v) {
+  static_assert(lanes == 2 || lanes == 4 || lanes == 8 || lanes == 16, "group size");
+  v += dpp<k_dpp_quad_xor1>(v);
+  if constexpr (lanes >= 4) v += dpp<k_dpp_quad_xor2>(v);
+  if constexpr (lanes >= 8) v += dpp<k_dpp_row_half_mirror>(v);
+  if constexpr (lanes >= 16) v += dpp<k_dpp_row_mirror>(v);
+  return v;
+}
+
+__device__ __forceinline__ float wave_shfl_xor(float v, int mask) {
+  return __shfl_xor(v, mask, k_wave);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// 16-byte global load/store.
+__device__ __forceinline__ uint4_t load16(const void *p) {
+  return *reinterpret_cast<const uint4_t *>(p);
+}
+__device__ __forceinline__ void store16(void *p, uint4_t v) {
+  *reinterpret_cast<uint4_t *>(p) = v;
+}
+
+}  // namespace emelk::dev

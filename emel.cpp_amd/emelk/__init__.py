@@ -1,0 +1,399 @@
+"""Python host binding of libemelk.so (the MI355X KV-cache hot path).
+
+ctypes over the C ABI declared in include/emelk.h.  The library is the only
+implementation: if it is missing, importing this module raises.  Device
+buffers are passed as raw HIP device addresses; helpers accept torch tensors
+and take their ``data_ptr()`` and the current torch stream.
+
+Mirrors the reference's memory/kv actor API (src/emel/memory/kv/sm.hpp:364-507,
+src/emel/memory/events.hpp:9-62): ``KvActor.process_event``-style methods take
+the same fields and return ``(accepted, error, out)``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional, Sequence
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.normpath(os.path.join(_HERE, "..", "lib", "libemelk.so"))
+
+ERR_NONE = 0
+ERR_INVALID_REQUEST = 1 << 0
+ERR_BACKEND = 1 << 1
+ERR_INTERNAL = 1 << 2
+ERR_OUT_OF_MEMORY = 1 << 3
+ERR_UNTRACKED = 1 << 4
+
+MAX_SEQUENCES = 256
+MAX_BLOCKS_PER_SEQUENCE = 4096
+MAX_BLOCKS = 32768
+INVALID_KV_BLOCK = 0xFFFF
+
+KV_F16 = 1
+KV_Q8_0 = 8
+
+c_i32p = ctypes.POINTER(ctypes.c_int32)
+COPY_BLOCK_FN = ctypes.CFUNCTYPE(ctypes.c_bool, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                 ctypes.c_void_p, c_i32p)
+COPY_STATE_FN = ctypes.CFUNCTYPE(ctypes.c_bool, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p,
+                                 c_i32p)
+
+
+class EvReserve(ctypes.Structure):
+    _fields_ = [("max_sequences", ctypes.c_int32), ("max_blocks", ctypes.c_int32),
+                ("block_tokens", ctypes.c_int32), ("error_out", c_i32p)]
+
+
+class EvAllocateSequence(ctypes.Structure):
+    _fields_ = [("seq_id", ctypes.c_int32), ("error_out", c_i32p)]
+
+
+class EvAllocateSlots(ctypes.Structure):
+    _fields_ = [("seq_id", ctypes.c_int32), ("token_count", ctypes.c_int32),
+                ("block_count_out", c_i32p), ("error_out", c_i32p),
+                ("copy_block", ctypes.c_void_p), ("copy_block_user_data", ctypes.c_void_p)]
+
+
+class EvBranchSequence(ctypes.Structure):
+    _fields_ = [("parent_seq_id", ctypes.c_int32), ("child_seq_id", ctypes.c_int32),
+                ("copy_state", ctypes.c_void_p), ("copy_state_user_data", ctypes.c_void_p),
+                ("error_out", c_i32p)]
+
+
+class EvFreeSequence(ctypes.Structure):
+    _fields_ = [("seq_id", ctypes.c_int32), ("error_out", c_i32p)]
+
+
+class EvRollbackSlots(ctypes.Structure):
+    _fields_ = [("seq_id", ctypes.c_int32), ("token_count", ctypes.c_int32),
+                ("block_count_out", c_i32p), ("error_out", c_i32p)]
+
+
+class Snapshot(ctypes.Structure):
+    _fields_ = [("max_sequences", ctypes.c_int32), ("block_tokens", ctypes.c_int32),
+                ("sequence_active", ctypes.c_uint8 * MAX_SEQUENCES),
+                ("sequence_length_values", ctypes.c_int32 * MAX_SEQUENCES),
+                ("sequence_kv_block_count", ctypes.c_int32 * MAX_SEQUENCES),
+                ("sequence_kv_blocks", (ctypes.c_uint16 * MAX_BLOCKS_PER_SEQUENCE) * MAX_SEQUENCES),
+                ("sequence_recurrent_slot", ctypes.c_int32 * MAX_SEQUENCES)]
+
+    # view::snapshot helpers (src/emel/memory/view.hpp:69-116)
+    def is_sequence_active(self, seq: int) -> bool:
+        return 0 <= seq < self.max_sequences and seq < MAX_SEQUENCES and \
+            self.sequence_active[seq] != 0
+
+    def sequence_length(self, seq: int) -> int:
+        return self.sequence_length_values[seq] if self.is_sequence_active(seq) else 0
+
+    def lookup_kv_block(self, seq: int, pos: int) -> int:
+        if not self.is_sequence_active(seq) or pos < 0 or self.block_tokens <= 0:
+            return -1
+        if pos >= self.sequence_length_values[seq]:
+            return -1
+        n = self.sequence_kv_block_count[seq]
+        if n <= 0 or n > MAX_BLOCKS_PER_SEQUENCE:
+            return -1
+        lb = pos // self.block_tokens
+        if lb >= n:
+            return -1
+        b = self.sequence_kv_blocks[seq][lb]
+        return -1 if b == INVALID_KV_BLOCK else int(b)
+
+    def lookup_recurrent_slot(self, seq: int) -> int:
+        return self.sequence_recurrent_slot[seq] if self.is_sequence_active(seq) else -1
+
+
+class EvCaptureView(ctypes.Structure):
+    _fields_ = [("snapshot_out", ctypes.POINTER(Snapshot)), ("error_out", c_i32p)]
+
+
+class EvEvictBlocks(ctypes.Structure):
+    _fields_ = [("seq_id", ctypes.c_int32), ("logical_blocks", c_i32p),
+                ("block_count", ctypes.c_int32), ("tokens_removed_out", c_i32p),
+                ("error_out", c_i32p)]
+
+
+class EvCompact(ctypes.Structure):
+    _fields_ = [("moves_out", c_i32p), ("max_moves", ctypes.c_int32),
+                ("move_count_out", c_i32p), ("error_out", c_i32p)]
+
+
+class KvBinding(ctypes.Structure):
+    _fields_ = [("actor", ctypes.c_void_p)] + [
+        (n, ctypes.c_void_p) for n in (
+            "dispatch_reserve", "dispatch_allocate_sequence", "dispatch_allocate_slots",
+            "dispatch_branch_sequence", "dispatch_free_sequence", "dispatch_rollback_slots",
+            "dispatch_capture_view")]
+
+
+class Geometry(ctypes.Structure):
+    _fields_ = [("n_layer", ctypes.c_int32), ("n_head", ctypes.c_int32),
+                ("n_head_kv", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+                ("block_tokens", ctypes.c_int32), ("max_blocks", ctypes.c_int32),
+                ("kv_type", ctypes.c_int32)]
+
+
+# (name, restype, argtypes) for every symbol include/emelk.h declares.
+_P = ctypes.c_void_p
+_SIGNATURES = [
+    ("emelk_kv_actor_create", _P, []),
+    ("emelk_kv_actor_destroy", None, [_P]),
+    ("emelk_kv_reserve", ctypes.c_bool, [_P, ctypes.POINTER(EvReserve)]),
+    ("emelk_kv_allocate_sequence", ctypes.c_bool, [_P, ctypes.POINTER(EvAllocateSequence)]),
+    ("emelk_kv_allocate_slots", ctypes.c_bool, [_P, ctypes.POINTER(EvAllocateSlots)]),
+    ("emelk_kv_branch_sequence", ctypes.c_bool, [_P, ctypes.POINTER(EvBranchSequence)]),
+    ("emelk_kv_free_sequence", ctypes.c_bool, [_P, ctypes.POINTER(EvFreeSequence)]),
+    ("emelk_kv_rollback_slots", ctypes.c_bool, [_P, ctypes.POINTER(EvRollbackSlots)]),
+    ("emelk_kv_capture_view", ctypes.c_bool, [_P, ctypes.POINTER(EvCaptureView)]),
+    ("emelk_kv_view", ctypes.POINTER(Snapshot), [_P]),
+    ("emelk_kv_lookup_kv_block", ctypes.c_int32, [_P, ctypes.c_int32, ctypes.c_int32]),
+    ("emelk_kv_evict_blocks", ctypes.c_bool, [_P, ctypes.POINTER(EvEvictBlocks)]),
+    ("emelk_kv_compact", ctypes.c_bool, [_P, ctypes.POINTER(EvCompact)]),
+    ("emelk_kv_bind", None, [_P, ctypes.POINTER(KvBinding)]),
+    ("emelk_kv_export_block_tables", ctypes.c_uint32,
+     [_P, c_i32p, ctypes.c_int32, ctypes.POINTER(ctypes.c_uint16), ctypes.c_int32]),
+    ("emelk_kv_set_free_order", ctypes.c_uint32,
+     [_P, ctypes.POINTER(ctypes.c_uint16), ctypes.c_int32]),
+    ("emelk_kv_block_refs", ctypes.c_int32, [_P, ctypes.c_int32]),
+    ("emelk_kv_free_count", ctypes.c_int32, [_P]),
+    ("emelk_kv_pool_bytes", ctypes.c_uint32,
+     [ctypes.POINTER(Geometry), ctypes.POINTER(ctypes.c_uint64)]),
+    ("emelk_kv_append", ctypes.c_uint32,
+     [ctypes.POINTER(Geometry), _P, _P, ctypes.c_int32, _P, _P, ctypes.c_int32, ctypes.c_int32,
+      _P, _P, ctypes.c_int32, _P]),
+    ("emelk_kv_gather", ctypes.c_uint32,
+     [ctypes.POINTER(Geometry), _P, _P, ctypes.c_int32, ctypes.c_int32, _P, _P, ctypes.c_int32,
+      _P, _P, ctypes.c_int32, _P]),
+    ("emelk_kv_copy_blocks", ctypes.c_uint32,
+     [ctypes.POINTER(Geometry), _P, _P, _P, ctypes.c_int32, _P]),
+    ("emelk_attn_decode_workspace_size", ctypes.c_uint32,
+     [ctypes.POINTER(Geometry), ctypes.c_int32, ctypes.c_int32, ctypes.POINTER(ctypes.c_uint64)]),
+    ("emelk_attn_decode", ctypes.c_uint32,
+     [ctypes.POINTER(Geometry), _P, _P, ctypes.c_int32, _P, _P, ctypes.c_int32, _P,
+      ctypes.c_int32, _P, ctypes.c_int32, ctypes.c_float, _P, ctypes.c_uint64, _P]),
+    ("emelk_attn_prefill_chunk", ctypes.c_uint32,
+     [ctypes.POINTER(Geometry), _P, _P, ctypes.c_int32, _P, _P, ctypes.c_int32, ctypes.c_int32,
+      _P, _P, ctypes.c_int32, ctypes.c_float, _P]),
+    ("emelk_kv_cache_create", ctypes.c_uint32,
+     [ctypes.POINTER(Geometry), _P, ctypes.POINTER(ctypes.c_void_p)]),
+    ("emelk_kv_cache_destroy", None, [_P]),
+    ("emelk_kv_cache_k_pool", _P, [_P]),
+    ("emelk_kv_cache_v_pool", _P, [_P]),
+    ("emelk_kv_cache_copy_block", ctypes.c_bool,
+     [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _P, c_i32p]),
+    ("emelk_build_info", ctypes.c_char_p, []),
+]
+SYMBOLS = [s[0] for s in _SIGNATURES]
+
+if not os.path.exists(LIB_PATH):
+    raise ImportError(f"libemelk.so not built at {LIB_PATH}: run __graft_entry__.build()")
+lib = ctypes.CDLL(LIB_PATH)
+for _name, _res, _args in _SIGNATURES:
+    _fn = getattr(lib, _name)
+    _fn.restype = _res
+    _fn.argtypes = _args
+
+
+def _i32():
+    return ctypes.c_int32(0)
+
+
+class KvActor:
+    """Host KV block-map actor (memory::kv::sm), one per cache."""
+
+    def __init__(self):
+        self.handle = lib.emelk_kv_actor_create()
+        if not self.handle:
+            raise MemoryError("emelk_kv_actor_create failed")
+        self._keep = []
+
+    def close(self):
+        if self.handle:
+            lib.emelk_kv_actor_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def reserve(self, max_sequences=0, max_blocks=0, block_tokens=16, error_out=True):
+        err = _i32()
+        ev = EvReserve(max_sequences, max_blocks, block_tokens,
+                       ctypes.pointer(err) if error_out else None)
+        return bool(lib.emelk_kv_reserve(self.handle, ctypes.byref(ev))), err.value
+
+    def allocate_sequence(self, seq_id, error_out=True):
+        err = _i32()
+        ev = EvAllocateSequence(seq_id, ctypes.pointer(err) if error_out else None)
+        return bool(lib.emelk_kv_allocate_sequence(self.handle, ctypes.byref(ev))), err.value
+
+    def allocate_slots(self, seq_id, token_count, copy_block=None, copy_block_user_data=None,
+                       block_count_out=True, error_out=True):
+        """Returns (accepted, error, block_count).  copy_block: a COPY_BLOCK_FN
+        instance or a raw function address (int)."""
+        err, cnt = _i32(), _i32()
+        cb = None
+        if copy_block is not None:
+            cb = copy_block if isinstance(copy_block, int) else ctypes.cast(copy_block,
+                                                                            ctypes.c_void_p).value
+        ev = EvAllocateSlots(seq_id, token_count, ctypes.pointer(cnt) if block_count_out else None,
+                             ctypes.pointer(err) if error_out else None, cb, copy_block_user_data)
+        ok = bool(lib.emelk_kv_allocate_slots(self.handle, ctypes.byref(ev)))
+        return ok, err.value, cnt.value
+
+    def branch_sequence(self, parent_seq_id, child_seq_id):
+        err = _i32()
+        ev = EvBranchSequence(parent_seq_id, child_seq_id, None, None, ctypes.pointer(err))
+        return bool(lib.emelk_kv_branch_sequence(self.handle, ctypes.byref(ev))), err.value
+
+    def free_sequence(self, seq_id):
+        err = _i32()
+        ev = EvFreeSequence(seq_id, ctypes.pointer(err))
+        return bool(lib.emelk_kv_free_sequence(self.handle, ctypes.byref(ev))), err.value
+
+    def rollback_slots(self, seq_id, token_count):
+        err, cnt = _i32(), _i32()
+        ev = EvRollbackSlots(seq_id, token_count, ctypes.pointer(cnt), ctypes.pointer(err))
+        ok = bool(lib.emelk_kv_rollback_slots(self.handle, ctypes.byref(ev)))
+        return ok, err.value, cnt.value
+
+    def capture_view(self, snapshot: Optional[Snapshot]):
+        err = _i32()
+        ev = EvCaptureView(ctypes.pointer(snapshot) if snapshot is not None else None,
+                           ctypes.pointer(err))
+        return bool(lib.emelk_kv_capture_view(self.handle, ctypes.byref(ev))), err.value
+
+    def view(self) -> Snapshot:
+        return lib.emelk_kv_view(self.handle).contents
+
+    def lookup_kv_block(self, seq_id, pos):
+        return int(lib.emelk_kv_lookup_kv_block(self.handle, seq_id, pos))
+
+    def evict_blocks(self, seq_id, logical_blocks: Sequence[int]):
+        err, removed = _i32(), _i32()
+        arr = (ctypes.c_int32 * max(1, len(logical_blocks)))(*logical_blocks)
+        ev = EvEvictBlocks(seq_id, arr, len(logical_blocks), ctypes.pointer(removed),
+                           ctypes.pointer(err))
+        ok = bool(lib.emelk_kv_evict_blocks(self.handle, ctypes.byref(ev)))
+        return ok, err.value, removed.value
+
+    def compact(self, max_moves=MAX_BLOCKS):
+        """Returns (accepted, error, moves) with moves a list of (src, dst)."""
+        err, cnt = _i32(), _i32()
+        buf = (ctypes.c_int32 * (2 * max(1, max_moves)))()
+        ev = EvCompact(buf, max_moves, ctypes.pointer(cnt), ctypes.pointer(err))
+        ok = bool(lib.emelk_kv_compact(self.handle, ctypes.byref(ev)))
+        moves = [(buf[2 * i], buf[2 * i + 1]) for i in range(cnt.value)]
+        return ok, err.value, moves
+
+    def export_block_tables(self, seq_ids: Sequence[int], stride: int):
+        import numpy as np
+        out = np.empty((len(seq_ids), stride), dtype=np.uint16)
+        ids = (ctypes.c_int32 * max(1, len(seq_ids)))(*seq_ids)
+        e = lib.emelk_kv_export_block_tables(
+            self.handle, ids, len(seq_ids),
+            out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)), stride)
+        if e != ERR_NONE:
+            raise ValueError(f"emelk_kv_export_block_tables error {e}")
+        return out
+
+    def set_free_order(self, order):
+        import numpy as np
+        arr = np.ascontiguousarray(order, dtype=np.uint16)
+        e = lib.emelk_kv_set_free_order(self.handle,
+                                        arr.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)),
+                                        len(arr))
+        if e != ERR_NONE:
+            raise ValueError(f"emelk_kv_set_free_order error {e}")
+
+    def block_refs(self, block):
+        return int(lib.emelk_kv_block_refs(self.handle, block))
+
+    def free_count(self):
+        return int(lib.emelk_kv_free_count(self.handle))
+
+    def binding(self) -> KvBinding:
+        b = KvBinding()
+        lib.emelk_kv_bind(self.handle, ctypes.byref(b))
+        return b
+
+
+# ---- device side (torch tensors as device buffers) -------------------------
+
+def geometry(n_layer, n_head, n_head_kv, head_dim, block_tokens, max_blocks, kv_type=KV_F16):
+    return Geometry(n_layer, n_head, n_head_kv, head_dim, block_tokens, max_blocks, kv_type)
+
+
+def pool_bytes(g: Geometry) -> int:
+    out = ctypes.c_uint64(0)
+    e = lib.emelk_kv_pool_bytes(ctypes.byref(g), ctypes.byref(out))
+    if e != ERR_NONE:
+        raise ValueError(f"invalid geometry (error {e})")
+    return int(out.value)
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream):
+    if stream is not None:
+        return ctypes.c_void_p(stream)
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _check(e, what):
+    if e != ERR_NONE:
+        raise RuntimeError(f"{what} failed with emel error {e}")
+
+
+def append(g, k_pool, v_pool, layer, k_rows, v_rows, positions, block_tables, stream=None):
+    """k_rows/v_rows: float32 [n_seq, n_tokens, n_head_kv*head_dim] on the device."""
+    n_seq, n_tokens = int(k_rows.shape[0]), int(k_rows.shape[1])
+    _check(lib.emelk_kv_append(ctypes.byref(g), _ptr(k_pool), _ptr(v_pool), layer, _ptr(k_rows),
+                               _ptr(v_rows), n_seq, n_tokens, _ptr(positions), _ptr(block_tables),
+                               int(block_tables.shape[1]), _stream(stream)), "emelk_kv_append")
+
+
+def gather(g, k_pool, v_pool, layer, lengths, block_tables, k_out, v_out, out_tokens,
+           stream=None):
+    _check(lib.emelk_kv_gather(ctypes.byref(g), _ptr(k_pool), _ptr(v_pool), layer,
+                               int(lengths.shape[0]), _ptr(lengths), _ptr(block_tables),
+                               int(block_tables.shape[1]), _ptr(k_out), _ptr(v_out), out_tokens,
+                               _stream(stream)), "emelk_kv_gather")
+
+
+def copy_blocks(g, k_pool, v_pool, moves, stream=None):
+    """moves: int32 [n, 2] device tensor of (src, dst) page ids."""
+    _check(lib.emelk_kv_copy_blocks(ctypes.byref(g), _ptr(k_pool), _ptr(v_pool), _ptr(moves),
+                                    int(moves.shape[0]), _stream(stream)),
+           "emelk_kv_copy_blocks")
+
+
+def decode_workspace_bytes(g, n_seq, max_kv_len) -> int:
+    out = ctypes.c_uint64(0)
+    _check(lib.emelk_attn_decode_workspace_size(ctypes.byref(g), n_seq, max_kv_len,
+                                                ctypes.byref(out)), "workspace_size")
+    return int(out.value)
+
+
+def decode(g, k_pool, v_pool, layer, q, out, kv_lens, max_kv_len, block_tables, scale,
+           workspace, stream=None):
+    _check(lib.emelk_attn_decode(ctypes.byref(g), _ptr(k_pool), _ptr(v_pool), layer, _ptr(q),
+                                 _ptr(out), int(q.shape[0]), _ptr(kv_lens), max_kv_len,
+                                 _ptr(block_tables), int(block_tables.shape[1]), scale,
+                                 _ptr(workspace), workspace.numel() * workspace.element_size(),
+                                 _stream(stream)), "emelk_attn_decode")
+
+
+def prefill_chunk(g, k_pool, v_pool, layer, q, out, q_start, block_tables, scale, stream=None):
+    """q/out: float32 [n_seq, n_q, n_head, head_dim]."""
+    _check(lib.emelk_attn_prefill_chunk(ctypes.byref(g), _ptr(k_pool), _ptr(v_pool), layer,
+                                        _ptr(q), _ptr(out), int(q.shape[0]), int(q.shape[1]),
+                                        _ptr(q_start), _ptr(block_tables),
+                                        int(block_tables.shape[1]), scale, _stream(stream)),
+           "emelk_attn_prefill_chunk")

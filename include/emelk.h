@@ -1,0 +1,288 @@
+/*
+ * emelk — MI355X (gfx950) KV-cache hot path for stateforward/emel.cpp.
+ *
+ * C ABI: plain pointers and sizes only.  Device pointers are HIP device
+ * addresses; `stream` is a hipStream_t passed as void* (NULL = the default
+ * stream).  Every entry point returns emel_error_type
+ * (reference include/emel/emel.h:11) with the memory/kv bit values of
+ * src/emel/memory/kv/errors.hpp:7-14, or `bool` where the reference event API
+ * returns bool.  Kernel entry points only enqueue work; they never
+ * synchronise the stream.
+ *
+ * Paths in citations are relative to the reference checkout.
+ */
+#ifndef EMELK_H
+#define EMELK_H
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef uint32_t emel_error_type; /* include/emel/emel.h:11 */
+
+/* src/emel/memory/kv/errors.hpp:7-14 */
+enum {
+  EMELK_ERR_NONE = 0u,
+  EMELK_ERR_INVALID_REQUEST = 1u << 0,
+  EMELK_ERR_BACKEND = 1u << 1,
+  EMELK_ERR_INTERNAL = 1u << 2,
+  EMELK_ERR_OUT_OF_MEMORY = 1u << 3,
+  EMELK_ERR_UNTRACKED = 1u << 4,
+};
+
+/* Geometry contract, src/emel/memory/view.hpp:10-19. */
+#define EMELK_MAX_SEQUENCES 256
+#define EMELK_MAX_BLOCKS_PER_SEQUENCE 4096
+#define EMELK_MAX_BLOCKS 32768
+#define EMELK_DEFAULT_BLOCK_TOKENS 16
+#define EMELK_INVALID_KV_BLOCK 0xFFFFu
+
+/* ------------------------------------------------------------------------ */
+/* Host KV block-map actor (src/emel/memory/kv/sm.hpp:364-507).             */
+/* Event structs are layout-identical to src/emel/memory/events.hpp:9-62.   */
+/* ------------------------------------------------------------------------ */
+
+typedef struct emelk_event_reserve { /* events.hpp:9-14 */
+  int32_t max_sequences;
+  int32_t max_blocks;
+  int32_t block_tokens;
+  int32_t *error_out;
+} emelk_event_reserve;
+
+typedef struct emelk_event_allocate_sequence { /* events.hpp:16-19 */
+  int32_t seq_id;
+  int32_t *error_out;
+} emelk_event_allocate_sequence;
+
+/* allocate_slots::copy_block_fn, events.hpp:22-26 */
+typedef bool (*emelk_copy_block_fn)(int32_t src_block, int32_t dst_block, int32_t block_tokens,
+                                    void *user_data, int32_t *error_out);
+
+typedef struct emelk_event_allocate_slots { /* events.hpp:21-34 */
+  int32_t seq_id;
+  int32_t token_count;
+  int32_t *block_count_out;
+  int32_t *error_out;
+  emelk_copy_block_fn copy_block;
+  void *copy_block_user_data;
+} emelk_event_allocate_slots;
+
+typedef bool (*emelk_copy_state_fn)(int32_t src_slot, int32_t dst_slot, void *user_data,
+                                    int32_t *error_out);
+
+typedef struct emelk_event_branch_sequence { /* events.hpp:36-45 */
+  int32_t parent_seq_id;
+  int32_t child_seq_id;
+  emelk_copy_state_fn copy_state;
+  void *copy_state_user_data;
+  int32_t *error_out;
+} emelk_event_branch_sequence;
+
+typedef struct emelk_event_free_sequence { /* events.hpp:47-50 */
+  int32_t seq_id;
+  int32_t *error_out;
+} emelk_event_free_sequence;
+
+typedef struct emelk_event_rollback_slots { /* events.hpp:52-57 */
+  int32_t seq_id;
+  int32_t token_count;
+  int32_t *block_count_out;
+  int32_t *error_out;
+} emelk_event_rollback_slots;
+
+/* view::snapshot, src/emel/memory/view.hpp:59-117 (same member order). */
+typedef struct emelk_view_snapshot {
+  int32_t max_sequences;
+  int32_t block_tokens;
+  uint8_t sequence_active[EMELK_MAX_SEQUENCES];
+  int32_t sequence_length_values[EMELK_MAX_SEQUENCES];
+  int32_t sequence_kv_block_count[EMELK_MAX_SEQUENCES];
+  uint16_t sequence_kv_blocks[EMELK_MAX_SEQUENCES][EMELK_MAX_BLOCKS_PER_SEQUENCE];
+  int32_t sequence_recurrent_slot[EMELK_MAX_SEQUENCES];
+} emelk_view_snapshot;
+
+typedef struct emelk_event_capture_view { /* events.hpp:59-62 */
+  emelk_view_snapshot *snapshot_out;
+  int32_t *error_out;
+} emelk_event_capture_view;
+
+/* New events (no counterpart in the reference, which never evicts or
+ * compacts; built on its copy_block mechanism, kv/actions.hpp:218-242). */
+typedef struct emelk_event_evict_blocks {
+  int32_t seq_id;
+  const int32_t *logical_blocks; /* distinct logical block indices of seq_id */
+  int32_t block_count;
+  int32_t *tokens_removed_out;
+  int32_t *error_out;
+} emelk_event_evict_blocks;
+
+typedef struct emelk_event_compact {
+  int32_t *moves_out;      /* host [max_moves][2] = (src_block, dst_block) */
+  int32_t max_moves;
+  int32_t *move_count_out;
+  int32_t *error_out;
+} emelk_event_compact;
+
+/* kv_binding, src/emel/memory/hybrid/context.hpp:21-30.  The reference's
+ * dispatch functions take `const event&`, which the platform C++ ABI passes
+ * as a pointer, so a filled emelk_kv_binding can be copied bit for bit into
+ * emel::memory::hybrid::kv_binding. */
+typedef struct emelk_kv_binding {
+  void *actor;
+  bool (*dispatch_reserve)(void *, const emelk_event_reserve *);
+  bool (*dispatch_allocate_sequence)(void *, const emelk_event_allocate_sequence *);
+  bool (*dispatch_allocate_slots)(void *, const emelk_event_allocate_slots *);
+  bool (*dispatch_branch_sequence)(void *, const emelk_event_branch_sequence *);
+  bool (*dispatch_free_sequence)(void *, const emelk_event_free_sequence *);
+  bool (*dispatch_rollback_slots)(void *, const emelk_event_rollback_slots *);
+  bool (*dispatch_capture_view)(void *, const emelk_event_capture_view *);
+} emelk_kv_binding;
+
+typedef struct emelk_kv_actor emelk_kv_actor;
+
+/* Construct / destroy (the reference sm is default-constructed, sm.hpp:370). */
+emelk_kv_actor *emelk_kv_actor_create(void);
+void emelk_kv_actor_destroy(emelk_kv_actor *actor);
+
+/* kv::sm::process_event overloads, src/emel/memory/kv/sm.hpp:372-465. */
+bool emelk_kv_reserve(emelk_kv_actor *actor, const emelk_event_reserve *ev);
+bool emelk_kv_allocate_sequence(emelk_kv_actor *actor, const emelk_event_allocate_sequence *ev);
+bool emelk_kv_allocate_slots(emelk_kv_actor *actor, const emelk_event_allocate_slots *ev);
+bool emelk_kv_branch_sequence(emelk_kv_actor *actor, const emelk_event_branch_sequence *ev);
+bool emelk_kv_free_sequence(emelk_kv_actor *actor, const emelk_event_free_sequence *ev);
+bool emelk_kv_rollback_slots(emelk_kv_actor *actor, const emelk_event_rollback_slots *ev);
+bool emelk_kv_capture_view(emelk_kv_actor *actor, const emelk_event_capture_view *ev);
+/* kv::sm::view() (sm.hpp:480-499): cached snapshot, refreshed when dirty. */
+const emelk_view_snapshot *emelk_kv_view(emelk_kv_actor *actor);
+/* snapshot::lookup_kv_block (view.hpp:87-109) on the cached view. */
+int32_t emelk_kv_lookup_kv_block(emelk_kv_actor *actor, int32_t seq_id, int32_t pos);
+
+bool emelk_kv_evict_blocks(emelk_kv_actor *actor, const emelk_event_evict_blocks *ev);
+bool emelk_kv_compact(emelk_kv_actor *actor, const emelk_event_compact *ev);
+
+/* hybrid::bind_kv_actor (hybrid/context.hpp:77-89). */
+void emelk_kv_bind(emelk_kv_actor *actor, emelk_kv_binding *binding_out);
+
+/* Copies the block rows of seq_ids[0..n_seq) into a host table
+ * [n_seq][table_stride] (entries past a sequence's block count are
+ * EMELK_INVALID_KV_BLOCK).  Replaces the per-decode snapshot walk of
+ * kv_addressing_from_request (text/generator/detail.hpp:1010-1014). */
+emel_error_type emelk_kv_export_block_tables(emelk_kv_actor *actor, const int32_t *seq_ids,
+                                             int32_t n_seq, uint16_t *table_out,
+                                             int32_t table_stride);
+
+/* Test and bench hook: replaces the free stack's pop order.  order[0] is
+ * popped first; it must be a permutation of the currently free block ids.
+ * Used to install the seeded random page permutations of the workloads
+ * through the real allocate_slots path. */
+emel_error_type emelk_kv_set_free_order(emelk_kv_actor *actor, const uint16_t *order,
+                                        int32_t count);
+
+/* Refcount of a physical block (kv/detail.hpp:46-97 block_pool). */
+int32_t emelk_kv_block_refs(emelk_kv_actor *actor, int32_t block_id);
+int32_t emelk_kv_free_count(emelk_kv_actor *actor);
+
+/* ------------------------------------------------------------------------ */
+/* Device page pool and kernels (gfx950).                                   */
+/* ------------------------------------------------------------------------ */
+
+enum { EMELK_KV_F16 = 1, EMELK_KV_Q8_0 = 8 };
+
+typedef struct emelk_kv_geometry {
+  int32_t n_layer;
+  int32_t n_head;      /* query heads */
+  int32_t n_head_kv;   /* key/value heads (GQA: n_head % n_head_kv == 0) */
+  int32_t head_dim;    /* 64 or 128 */
+  int32_t block_tokens;/* tokens per page */
+  int32_t max_blocks;  /* pages in the pool */
+  int32_t kv_type;     /* EMELK_KV_F16 or EMELK_KV_Q8_0 */
+} emelk_kv_geometry;
+
+/* Bytes of one pool (K or V; both have the same size).  Layout:
+ *   f16 : [layer][page][kv_head][block_tokens][head_dim] halves
+ *   q8_0: [layer][page][kv_head] regions of block_tokens*head_dim int8 values
+ *         followed by block_tokens*head_dim/32 f16 scales (GGUF q8_0 content,
+ *         split into value and scale planes per page and head). */
+emel_error_type emelk_kv_pool_bytes(const emelk_kv_geometry *g, uint64_t *bytes_out);
+
+/* store_attention_kv_cache (text/generator/detail.hpp:3294-3332) for a batch:
+ * k_rows/v_rows are fp32 [n_seq][n_tokens][n_head_kv*head_dim]; token t of
+ * sequence s lands at logical position positions[s] + t through
+ * block_tables[s*table_stride + pos/block_tokens].  f16 pools: RNE rounding
+ * (quant::fp32_to_fp16, kernel/detail.hpp:372-392).  q8_0 pools: per 32
+ * values quantize_row_q8_0_strided (kernel/detail.hpp:804-824). */
+emel_error_type emelk_kv_append(const emelk_kv_geometry *g, void *k_pool, void *v_pool,
+                                int32_t layer, const float *k_rows, const float *v_rows,
+                                int32_t n_seq, int32_t n_tokens, const int32_t *positions,
+                                const uint16_t *block_tables, int32_t table_stride, void *stream);
+
+/* Block-table gather: logical tokens [0, lengths[s]) of layer `layer` into
+ * dense head-major outputs [n_seq][n_head_kv][out_tokens][...]: f16 rows of
+ * head_dim halves, or GGUF block_q8_0 rows (head_dim/32 blocks of 34 bytes,
+ * kernel/detail.hpp:226-229).  Addressing is physical_kv_position +
+ * flash_layer_cache_head_position_offset (text/generator/detail.hpp:2976-3048). */
+emel_error_type emelk_kv_gather(const emelk_kv_geometry *g, const void *k_pool,
+                                const void *v_pool, int32_t layer, int32_t n_seq,
+                                const int32_t *lengths, const uint16_t *block_tables,
+                                int32_t table_stride, void *k_out, void *v_out,
+                                int32_t out_tokens, void *stream);
+
+/* Batched page copy for every layer, K and V: moves is device int32
+ * [n_moves][2] = (src_block, dst_block).  copy_attention_kv_block
+ * (text/generator/detail.hpp:3334-3417) applied to many pages in one launch.
+ * Sources and destinations must be disjoint sets (eviction compaction and the
+ * copy-on-write tail split both satisfy this). */
+emel_error_type emelk_kv_copy_blocks(const emelk_kv_geometry *g, void *k_pool, void *v_pool,
+                                     const int32_t *moves, int32_t n_moves, void *stream);
+
+/* Split-K flash-decode GQA attention for one layer; replaces compute_attention
+ * (text/generator/detail.hpp:3153-3230) and the flash route
+ * (kernel/detail.hpp:5238-5291).  q: fp32 [n_seq][n_head][head_dim] (rounded
+ * to fp16 on load, as round_q_for_nonflash does); out: fp32, same shape.
+ * kv_lens: device int32 [n_seq], tokens to attend (position + 1), each in
+ * [1, max_kv_len].  scale multiplies q.k.  workspace: device scratch of
+ * emelk_attn_decode_workspace_size bytes. */
+emel_error_type emelk_attn_decode_workspace_size(const emelk_kv_geometry *g, int32_t n_seq,
+                                                 int32_t max_kv_len, uint64_t *bytes_out);
+emel_error_type emelk_attn_decode(const emelk_kv_geometry *g, const void *k_pool,
+                                  const void *v_pool, int32_t layer, const float *q, float *out,
+                                  int32_t n_seq, const int32_t *kv_lens, int32_t max_kv_len,
+                                  const uint16_t *block_tables, int32_t table_stride, float scale,
+                                  void *workspace, uint64_t workspace_bytes, void *stream);
+
+/* Chunked-prefill attention on MFMA for one layer (f16 pools): q fp32
+ * [n_seq][n_q][n_head][head_dim]; row r of sequence s attends causally to
+ * logical positions [0, q_start[s] + r] (the chunk must already be appended).
+ * Replaces the per-row store + attend loop of run_prefill
+ * (text/generator/detail.hpp:4297-4372). */
+emel_error_type emelk_attn_prefill_chunk(const emelk_kv_geometry *g, const void *k_pool,
+                                         const void *v_pool, int32_t layer, const float *q,
+                                         float *out, int32_t n_seq, int32_t n_q,
+                                         const int32_t *q_start, const uint16_t *block_tables,
+                                         int32_t table_stride, float scale, void *stream);
+
+/* Device KV owner: allocates both pools (hipMalloc) and serves as the
+ * allocate_slots copy_block callback target (text/generator/context.hpp:36-50). */
+typedef struct emelk_kv_cache emelk_kv_cache;
+emel_error_type emelk_kv_cache_create(const emelk_kv_geometry *g, void *stream,
+                                      emelk_kv_cache **cache_out);
+void emelk_kv_cache_destroy(emelk_kv_cache *cache);
+void *emelk_kv_cache_k_pool(emelk_kv_cache *cache);
+void *emelk_kv_cache_v_pool(emelk_kv_cache *cache);
+/* emelk_copy_block_fn: user_data is an emelk_kv_cache*.  Enqueues the copy of
+ * one page (all layers, K and V) on the cache's stream. */
+bool emelk_kv_cache_copy_block(int32_t src_block, int32_t dst_block, int32_t block_tokens,
+                               void *user_data, int32_t *error_out);
+
+/* Library version and the device the kernels were built for. */
+const char *emelk_build_info(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EMELK_H */
