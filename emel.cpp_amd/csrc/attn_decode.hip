@@ -20,10 +20,10 @@
 //   one partial (m, l, acc[D]) per (sequence, head, split) is written.
 //   A second kernel merges the splits.
 //
-// q8_0 pools: identical structure; the 16 int8 values of a lane are turned
-// into exact fp16 with a byte-permute + packed subtract, the lane's block
-// scale multiplies its partial score, and V scales fold into the fp16
-// probabilities (p * d_v).
+// q8_0 pools: identical structure; for scores the 16 int8 values of a lane
+// are turned into exact fp16 with a byte-permute + packed subtract and the
+// lane's block scale multiplies its partial score; for P.V the int8 values
+// go to fp32 and the token scale folds into an fp32 weight p * d_v.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -68,6 +68,18 @@ __device__ __forceinline__ void i8x16_to_half(const uint4_t w, half2_t out[8]) {
     const uint32_t u = ws[i] ^ 0x80808080u;
     out[2 * i] = as_half2(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - bias;
     out[2 * i + 1] = as_half2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - bias;
+  }
+}
+
+// 16 int8 -> 16 fp32 (exact).
+__device__ __forceinline__ void i8x16_to_float(const uint4_t w, float out[16]) {
+  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      out[4 * i + b] = static_cast<float>(static_cast<int8_t>((ws[i] >> (8 * b)) & 0xFFu));
+    }
   }
 }
 
@@ -223,16 +235,28 @@ __global__ __launch_bounds__(k_threads, 2) void decode_kernel(decode_params P) {
       s1[h] = group_sum<LPT>(b);
     }
 
-    // V pairs (token0, token1) per dimension
-    half2_t vh0[8], vh1[8];
-    float vs0, vs1;
-    to_half<D, Q8>(v0, vh0, vs0);
-    to_half<D, Q8>(v1, vh1, vs1);
-    half2_t vlo[8], vhi[8];
+    // P.V.  f16 pools: V values of the two tokens paired per dimension and
+    // contracted with the fp16 pair (p0, p1) by v_dot2_f32_f16.  q8_0 pools:
+    // the int8 values are exact in fp32 and the per-token scale folds into
+    // an fp32 weight p*d_v, so nothing is rounded to fp16 (an fp16 p*d_v
+    // would cost up to ~2^-11 * 127 * d_v per dominant token).
+    [[maybe_unused]] half2_t vlo[8], vhi[8];
+    [[maybe_unused]] float vf0[16], vf1[16];
+    [[maybe_unused]] float vs0 = 1.0f, vs1 = 1.0f;
+    if constexpr (!Q8) {
+      half2_t vh0[8], vh1[8];
+      to_half<D, Q8>(v0, vh0, vs0);
+      to_half<D, Q8>(v1, vh1, vs1);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      vlo[j] = as_half2(__builtin_amdgcn_perm(as_u32(vh1[j]), as_u32(vh0[j]), 0x05040100u));
-      vhi[j] = as_half2(__builtin_amdgcn_perm(as_u32(vh1[j]), as_u32(vh0[j]), 0x07060302u));
+      for (int j = 0; j < 8; ++j) {
+        vlo[j] = as_half2(__builtin_amdgcn_perm(as_u32(vh1[j]), as_u32(vh0[j]), 0x05040100u));
+        vhi[j] = as_half2(__builtin_amdgcn_perm(as_u32(vh1[j]), as_u32(vh0[j]), 0x07060302u));
+      }
+    } else {
+      i8x16_to_float(v0.a, vf0);
+      i8x16_to_float(v1.a, vf1);
+      vs0 = f16_bits_to_f32(static_cast<uint16_t>(v0.d));
+      vs1 = f16_bits_to_f32(static_cast<uint16_t>(v1.d));
     }
 
 #pragma unroll
@@ -250,16 +274,18 @@ __global__ __launch_bounds__(k_threads, 2) void decode_kernel(decode_params P) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[h][i] *= alpha;
       }
-      half2_t pp;
       if constexpr (Q8) {
-        pp = pack_half2(p0 * vs0, p1 * vs1);
-      } else {
-        pp = pack_half2(p0, p1);
-      }
+        const float w0 = p0 * vs0;
+        const float w1 = p1 * vs1;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        acc[h][2 * j] = dot2(pp, vlo[j], acc[h][2 * j]);
-        acc[h][2 * j + 1] = dot2(pp, vhi[j], acc[h][2 * j + 1]);
+        for (int i = 0; i < 16; ++i) acc[h][i] = fmaf(w1, vf1[i], fmaf(w0, vf0[i], acc[h][i]));
+      } else {
+        const half2_t pp = pack_half2(p0, p1);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          acc[h][2 * j] = dot2(pp, vlo[j], acc[h][2 * j]);
+          acc[h][2 * j + 1] = dot2(pp, vhi[j], acc[h][2 * j + 1]);
+        }
       }
     }
 

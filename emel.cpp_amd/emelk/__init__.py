@@ -188,6 +188,15 @@ SYMBOLS = [s[0] for s in _SIGNATURES]
 
 if not os.path.exists(LIB_PATH):
     raise ImportError(f"libemelk.so not built at {LIB_PATH}: run __graft_entry__.build()")
+# PyTorch-ROCm wheels ship their own HIP/HSA runtimes.  Loading torch first
+# makes libemelk.so's libamdhip64.so.7 / libhsa-runtime64.so.1 dependencies
+# resolve (by SONAME) to the runtime torch already holds, so streams and
+# device pointers from torch are valid here; loading libemelk.so first would
+# put a second HIP runtime in the process.
+try:
+    import torch  # noqa: F401
+except ImportError:  # plain C/C++ or numpy callers: the system ROCm runtime is used
+    pass
 lib = ctypes.CDLL(LIB_PATH)
 for _name, _res, _args in _SIGNATURES:
     _fn = getattr(lib, _name)

@@ -232,7 +232,8 @@ static void load_q8_0_row(const void *cache, const uint16_t *blocks, int32_t bt,
 }
 
 static int compute_attention_generic(const float *q, const void *key_cache, const void *value_cache,
-                                     orc_row_loader load, const uint16_t *blocks, int32_t bt,
+                                     orc_row_loader load, int round_v, const uint16_t *blocks,
+                                     int32_t bt,
                                      int32_t n_head, int32_t n_head_kv, int32_t head_dim,
                                      int32_t position_limit, int32_t n_ctx, float inv_scale,
                                      float *out, float *scratch) {
@@ -273,7 +274,9 @@ static int compute_attention_generic(const float *q, const void *key_cache, cons
     for (int32_t p = 0; p < position_limit; ++p) {
       load(value_cache, blocks, bt, kv_dim, p, kv_head, head_dim, vrow);
       const double w = (double)fp16r(rounded[p]);
-      for (int32_t d = 0; d < head_dim; ++d) accv[d] += (double)fp16r(vrow[d]) * w;
+      for (int32_t d = 0; d < head_dim; ++d) {
+        accv[d] += (double)(round_v ? fp16r(vrow[d]) : vrow[d]) * w;
+      }
     }
     /* padded columns contribute fp16r(0) * p = +0.0 to each sum: no-op */
     for (int32_t d = 0; d < head_dim; ++d) out[(int64_t)head * head_dim + d] = (float)accv[d];
@@ -288,21 +291,24 @@ int orc_compute_attention_f16(const float *q, const uint16_t *key_cache,
                               int32_t bt, int32_t n_head, int32_t n_head_kv,
                               int32_t head_dim, int32_t position_limit, int32_t n_ctx,
                               float inv_scale, float *out, float *scratch) {
-  return compute_attention_generic(q, key_cache, value_cache, load_f16_row, blocks, bt, n_head,
+  return compute_attention_generic(q, key_cache, value_cache, load_f16_row, 1, blocks, bt, n_head,
                                    n_head_kv, head_dim, position_limit, n_ctx, inv_scale, out,
                                    scratch);
 }
 
 /* q8_0 cache: identical arithmetic, with the K/V values produced by
- * dequantize_row_q8_0.  The PV dot of the reference rounds its value operand
- * to fp16 (dot_product_ggml_f16_scores); that rounding is kept here so the
- * route is the f16 route applied to dequantized rows. */
+ * dequantize_row_q8_0.  The reference's PV dot rounds its value operand to
+ * fp16 (dot_product_ggml_f16_scores) because its cache holds fp16 values, for
+ * which that rounding is the identity; dequantized q8_0 values (d * q, up to
+ * 19 significant bits) are not fp16 values, so here they enter the double
+ * sum unrounded — the only rounding kept is the reference's own (q and the
+ * normalised probabilities to fp16). */
 int orc_compute_attention_q8_0(const float *q, const orc_block_q8_0 *key_cache,
                                const orc_block_q8_0 *value_cache, const uint16_t *blocks,
                                int32_t bt, int32_t n_head, int32_t n_head_kv,
                                int32_t head_dim, int32_t position_limit, int32_t n_ctx,
                                float inv_scale, float *out, float *scratch) {
-  return compute_attention_generic(q, key_cache, value_cache, load_q8_0_row, blocks, bt, n_head,
+  return compute_attention_generic(q, key_cache, value_cache, load_q8_0_row, 0, blocks, bt, n_head,
                                    n_head_kv, head_dim, position_limit, n_ctx, inv_scale, out,
                                    scratch);
 }

@@ -22,6 +22,7 @@ class Scenario:
         self.kv_type = kv_type
         self.kv_dim = n_kv * head_dim
         self.rng = np.random.default_rng(seed)
+        perm_rng = np.random.default_rng(seed + 7919)  # page placement only
         self.device = device
         need = sum(-(-n // block_tokens) for n in self.lens)
         self.max_blocks = need + extra_blocks
@@ -29,7 +30,7 @@ class Scenario:
         ok, err = self.actor.reserve(max(self.n_seq, 1), self.max_blocks, block_tokens)
         assert ok, err
         if not identity:
-            self.actor.set_free_order(self.rng.permutation(self.max_blocks).astype(np.uint16))
+            self.actor.set_free_order(perm_rng.permutation(self.max_blocks).astype(np.uint16))
         for s, n in enumerate(self.lens):
             assert self.actor.allocate_sequence(s)[0]
             ok, err, _ = self.actor.allocate_slots(s, n)
@@ -136,7 +137,11 @@ class Scenario:
         return out
 
     def ideal_decode(self, layer, q, scale=None):
+        """fp64 attention on exactly the operands both routes consume: the
+        stored K/V values and q rounded to fp16 (round_q_for_nonflash,
+        text/generator/detail.hpp:2898-2903)."""
         scale = (1.0 / np.sqrt(self.D)) if scale is None else scale
+        q = oracle.fp16_to_fp32(oracle.fp32_to_fp16(q))
         out = np.zeros((self.n_seq, self.n_head * self.D), np.float32)
         for s, n in enumerate(self.lens):
             if self.kv_type == emelk.KV_F16:

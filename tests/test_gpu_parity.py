@@ -142,6 +142,7 @@ def test_copy_blocks_and_compaction_are_bit_exact(device):
 def test_copy_block_callback_splits_shared_tail(device):
     banner("copy_block callback through allocate_slots")
     import ctypes
+    import os
     import torch
     g = emelk.geometry(2, 8, 2, 64, 16, 8)
     cache = ctypes.c_void_p()
@@ -171,7 +172,7 @@ def test_copy_block_callback_splits_shared_tail(device):
         src, dst = a.lookup_kv_block(0, 0), a.lookup_kv_block(1, 0)
         assert src != dst
         pb = emelk.pool_bytes(g)
-        hip = ctypes.CDLL("libamdhip64.so")
+        hip = ctypes.CDLL("libamdhip64.so.7", mode=os.RTLD_NOLOAD)  # the loaded runtime
         for pool in (kp, vp):
             host = np.zeros(pb, dtype=np.uint8)
             assert hip.hipMemcpy(ctypes.c_void_p(host.ctypes.data), ctypes.c_void_p(pool),
