@@ -291,3 +291,51 @@ def test_decode_is_invariant_to_page_placement(device):
     q = np.random.default_rng(4).standard_normal((2, 32 * 128)).astype(np.float32)
     assert not np.array_equal(a.tables_host, b.tables_host)
     np.testing.assert_array_equal(a.gpu_decode(0, q), b.gpu_decode(0, q))
+
+
+# --------------------------------------------------------------- prefill ----
+
+def _prefill_case(device, n_head, n_kv, D, bt, q_starts, n_q, seed):
+    import torch
+    lens = [s + n_q for s in q_starts]
+    sc = Scenario(n_layer=1, n_head=n_head, n_kv=n_kv, head_dim=D, block_tokens=bt, lens=lens,
+                  seed=seed)
+    rng = np.random.default_rng(seed + 1)
+    q = rng.standard_normal((sc.n_seq, n_q, n_head, D)).astype(np.float32)
+    qd = torch.from_numpy(q).to(device)
+    out = torch.full_like(qd, float("nan"))
+    qs = torch.tensor(q_starts, dtype=torch.int32, device=device)
+    scale = 1.0 / np.sqrt(D)
+    emelk.prefill_chunk(sc.g, sc.k_pool, sc.v_pool, 0, qd, out, qs, sc.tables, scale)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    kc, vc = sc.oracle_cache(0)
+    want = np.zeros_like(got)
+    ideal = np.zeros_like(got)
+    for s in range(sc.n_seq):
+        kf = oracle.fp16_to_fp32(oracle.fp32_to_fp16(sc.k_rows[0][s]))
+        vf = oracle.fp16_to_fp32(oracle.fp32_to_fp16(sc.v_rows[0][s]))
+        for r in range(n_q):
+            limit = q_starts[s] + r + 1  # row r attends causally to [0, q_start + r]
+            want[s, r] = oracle.compute_attention_f16(
+                q[s, r].ravel(), kc, vc, sc.tables_host[s], bt, n_head, n_kv, D, limit, limit,
+                scale).reshape(n_head, D)
+            qr = oracle.fp16_to_fp32(oracle.fp32_to_fp16(q[s, r].ravel()))
+            ideal[s, r] = oracle.attention_f64(qr, kf[:limit], vf[:limit], n_head, n_kv, D, limit,
+                                               scale).reshape(n_head, D)
+    assert_close(got, want, what="prefill gpu vs reference per-row route")
+    assert_close(got, ideal, what="prefill gpu vs fp64 ideal")
+
+
+def test_prefill_chunk_config5_shape(device):
+    # Llama-3-8B heads, 32-token pages; prefixes not multiples of the tile,
+    # chunk of 96 rows (three 32-row blocks)
+    banner("prefill chunk llama-3-8b heads, prefixes [200, 1000], 96 rows")
+    _prefill_case(device, 32, 8, 128, 32, [200, 1000], 96, seed=31)
+
+
+def test_prefill_chunk_edges(device):
+    banner("prefill chunk edges: empty prefix, ragged rows, G=2 and G=1, D=64")
+    _prefill_case(device, 8, 4, 64, 16, [0, 33], 40, seed=32)
+    _prefill_case(device, 4, 4, 128, 16, [5], 7, seed=33)
+    _prefill_case(device, 16, 2, 128, 32, [64], 33, seed=34)  # G=8
