@@ -38,9 +38,17 @@ namespace {
 
 using namespace emelk::dev;
 
-constexpr int k_threads = 256;
-constexpr int k_waves = k_threads / k_wave;
+constexpr int k_max_wpb = 8;  // waves (KV heads) per workgroup
 constexpr int k_max_split_pages = 1024;
+
+// Waves per workgroup = KV heads per workgroup: min(n_head_kv, 8) when it
+// divides n_head_kv, else 1.
+inline int32_t waves_per_block(int32_t n_head_kv) {
+  for (int32_t w = k_max_wpb; w > 1; w >>= 1) {
+    if (n_head_kv % w == 0) return w;
+  }
+  return 1;
+}
 
 struct decode_params {
   pool_layout L;
@@ -71,15 +79,14 @@ __device__ __forceinline__ void i8x16_to_half(const uint4_t w, half2_t out[8]) {
   }
 }
 
-// 16 int8 -> 16 fp32 (exact).
-__device__ __forceinline__ void i8x16_to_float(const uint4_t w, float out[16]) {
-  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+// 16 int8 -> 16 fp32 values q + 128 (exact; one v_cvt_f32_ubyte each).
+__device__ __forceinline__ void u8x16_biased_to_float(const uint4_t w, float out[16]) {
+  const uint32_t ws[4] = {w.x ^ 0x80808080u, w.y ^ 0x80808080u, w.z ^ 0x80808080u,
+                          w.w ^ 0x80808080u};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      out[4 * i + b] = static_cast<float>(static_cast<int8_t>((ws[i] >> (8 * b)) & 0xFFu));
-    }
+    for (int b = 0; b < 4; ++b) out[4 * i + b] = static_cast<float>((ws[i] >> (8 * b)) & 0xFFu);
   }
 }
 
@@ -95,17 +102,31 @@ struct row_regs<D, true> {
   uint32_t d;    // scale bits (low 16)
 };
 
+// Lane dims.  f16 rows (2*D bytes): the lane's 16 dims are two runs of 8,
+// [8*l, 8*l+8) and [D/2 + 8*l, D/2 + 8*l + 8) for lane l of the row, so each
+// load instruction of a wave covers whole contiguous half rows (full 128-byte
+// lines at D = 128).  q8_0 rows (D bytes): one run [16*l, 16*l + 16).
+template <int D, bool Q8>
+__device__ __forceinline__ int lane_dim(int lane_in_row, int i) {
+  if constexpr (Q8) {
+    return 16 * lane_in_row + i;
+  } else {
+    return (i < 8 ? 0 : D / 2 - 8) + 8 * lane_in_row + i;
+  }
+}
+
 template <int D, bool Q8>
 __device__ __forceinline__ void load_row(const uint8_t *__restrict__ region_base, int32_t off,
-                                         int32_t dim0, int32_t bt, row_regs<D, Q8> &r) {
+                                         int32_t lane_in_row, int32_t bt, row_regs<D, Q8> &r) {
   if constexpr (!Q8) {
-    const uint8_t *p = region_base + (static_cast<uint64_t>(off) * D + dim0) * 2u;
-    r.a = load16(p);
-    r.b = load16(p + 16);
+    const uint8_t *p = region_base + static_cast<uint64_t>(off) * D * 2u + lane_in_row * 16;
+    r.a = load16_stream(p);
+    r.b = load16_stream(p + D);
   } else {
-    r.a = load16(region_base + static_cast<uint64_t>(off) * D + dim0);
+    const int32_t dim0 = 16 * lane_in_row;
+    r.a = load16_stream(region_base + static_cast<uint64_t>(off) * D + dim0);
     const uint16_t *sc = reinterpret_cast<const uint16_t *>(region_base + static_cast<uint64_t>(bt) * D);
-    r.d = sc[off * (D / 32) + dim0 / 32];
+    r.d = load2_stream(sc + off * (D / 32) + dim0 / 32);
   }
 }
 
@@ -122,20 +143,142 @@ __device__ __forceinline__ void to_half(const row_regs<D, Q8> &r, half2_t h[8], 
   }
 }
 
+// Lazy rescaling: the running reference max of a head only moves when a
+// score exceeds it by more than k_rescale (log2 units), so exp2(y - m) stays
+// <= 2^k_rescale (fine for fp32 sums and for the fp16 P operand) and the
+// accumulator rescale is skipped on almost every tile.  Any reference value
+// gives the same softmax once l and acc are merged against it.
+constexpr float k_rescale = 8.0f;
+
 template <int D, int G, bool Q8>
-__global__ __launch_bounds__(k_threads, 2) void decode_kernel(decode_params P) {
-  constexpr int LPT = D / 16;           // lanes per token row
-  constexpr int NG = k_threads / LPT;   // token groups per workgroup
-  constexpr int TT = 2 * NG;            // tokens per tile
+struct decode_state {
+  half2_t qh[G][8];  // fp16 q, 16 dims of each head
+  float m[G];        // reference max (log2 domain, scale folded in)
+  float l[G];
+  float acc[G][16];
+  float corr[G];     // q8_0: sum of P.V weights (undoes the +128 byte bias)
+};
+
+template <int D, bool Q8>
+struct tile_regs {
+  row_regs<D, Q8> k0, k1, v0, v1;
+};
+
+// One tile: two tokens per lane group (t0, t1).  MASKED handles the split's
+// tail and invalid pages (ok0/ok1 false).
+template <int D, int G, bool Q8, bool MASKED>
+__device__ __forceinline__ void consume_tile(decode_state<D, G, Q8> &S, const tile_regs<D, Q8> &T,
+                                             bool ok0, bool ok1, float c) {
+  constexpr int LPT = D / 16;
+  half2_t kh0[8], kh1[8];
+  float ks0, ks1;
+  to_half<D, Q8>(T.k0, kh0, ks0);
+  to_half<D, Q8>(T.k1, kh1, ks1);
+  float y0[G], y1[G];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    float a = 0.0f, b = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      a = dot2(S.qh[h][j], kh0[j], a);
+      b = dot2(S.qh[h][j], kh1[j], b);
+    }
+    if constexpr (Q8) {  // each lane's 16 values share one block scale
+      a *= ks0;
+      b *= ks1;
+    }
+    y0[h] = group_sum<LPT>(a) * c;
+    y1[h] = group_sum<LPT>(b) * c;
+    if constexpr (MASKED) {
+      y0[h] = ok0 ? y0[h] : -INFINITY;
+      y1[h] = ok1 ? y1[h] : -INFINITY;
+    }
+  }
+
+  // V operands: f16 pools pair the two tokens per dimension for
+  // v_dot2_f32_f16 with the fp16 pair (p0, p1); q8_0 pools keep the bytes
+  // biased by +128 (exact in fp32 via v_cvt_f32_ubyte) and fold the token
+  // scale into an fp32 weight, so nothing on the q8_0 P.V path is rounded.
+  [[maybe_unused]] half2_t vlo[8], vhi[8];
+  [[maybe_unused]] float vf0[16], vf1[16];
+  [[maybe_unused]] float vs0 = 1.0f, vs1 = 1.0f;
+  if constexpr (!Q8) {
+    const uint32_t w0[8] = {T.v0.a.x, T.v0.a.y, T.v0.a.z, T.v0.a.w,
+                            T.v0.b.x, T.v0.b.y, T.v0.b.z, T.v0.b.w};
+    const uint32_t w1[8] = {T.v1.a.x, T.v1.a.y, T.v1.a.z, T.v1.a.w,
+                            T.v1.b.x, T.v1.b.y, T.v1.b.z, T.v1.b.w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      vlo[j] = as_half2(__builtin_amdgcn_perm(w1[j], w0[j], 0x05040100u));
+      vhi[j] = as_half2(__builtin_amdgcn_perm(w1[j], w0[j], 0x07060302u));
+    }
+  } else {
+    u8x16_biased_to_float(T.v0.a, vf0);
+    u8x16_biased_to_float(T.v1.a, vf1);
+    vs0 = f16_bits_to_f32(static_cast<uint16_t>(T.v0.d));
+    vs1 = f16_bits_to_f32(static_cast<uint16_t>(T.v1.d));
+  }
+
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    const float mx = fmaxf(y0[h], y1[h]);
+    if (mx > S.m[h] + k_rescale) {
+      const float alpha = fast_exp2(S.m[h] - mx);  // 0 on the first valid token
+      S.m[h] = mx;
+      S.l[h] *= alpha;
+      if constexpr (Q8) S.corr[h] *= alpha;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) S.acc[h][i] *= alpha;
+    }
+    float p0 = fast_exp2(y0[h] - S.m[h]);
+    float p1 = fast_exp2(y1[h] - S.m[h]);
+    if constexpr (MASKED) {  // masked tokens, also while m is still -inf
+      p0 = y0[h] == -INFINITY ? 0.0f : p0;
+      p1 = y1[h] == -INFINITY ? 0.0f : p1;
+    }
+    S.l[h] += p0 + p1;
+    if constexpr (Q8) {
+      const float w0 = p0 * vs0;
+      const float w1 = p1 * vs1;
+      S.corr[h] += w0 + w1;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) S.acc[h][i] = fmaf(w1, vf1[i], fmaf(w0, vf0[i], S.acc[h][i]));
+    } else {
+      const half2_t pp = pack_half2(p0, p1);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        S.acc[h][2 * j] = dot2(pp, vlo[j], S.acc[h][2 * j]);
+        S.acc[h][2 * j + 1] = dot2(pp, vhi[j], S.acc[h][2 * j + 1]);
+      }
+    }
+  }
+}
+
+// Workgroup = WPB waves = WPB KV heads of one sequence over one split of
+// its context; wave w owns KV head blockIdx.y*WPB + w and its G query heads.
+// All waves walk the same pages at the same time, so a workgroup reads
+// whole pages (every head's slice) rather than one 8 KiB head slice per
+// page: measured on MI355X this access order streams ~15% faster from HBM.
+// Each wave merges its own token groups with shuffles; no cross-wave step.
+//
+// UNIFORM: block_tokens is a multiple of the wave's lane-group count NGW, so
+// every row of a (tile, half) lies in one page: the page id is moved to a
+// scalar register once per half-tile and each lane adds a fixed offset.
+template <int D, int G, bool Q8, bool UNIFORM, int WPB>
+__global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
+  constexpr int LPT = D / 16;         // lanes per token row
+  constexpr int NGW = k_wave / LPT;   // token groups per wave
+  constexpr int TT = 2 * NGW;         // tokens per wave tile
+  constexpr int NT = WPB * k_wave;
 
   __shared__ uint32_t s_pages[k_max_split_pages];
-  __shared__ float s_acc[k_waves][G][D];
-  __shared__ float s_ml[k_waves][G][2];
 
   const int32_t split = blockIdx.x;
-  const int32_t kvh = blockIdx.y;
   const int32_t seq = blockIdx.z;
   const int32_t tid = threadIdx.x;
+  const int32_t wave = tid / k_wave;
+  const int32_t lane = tid % k_wave;
+  const int32_t kvh = blockIdx.y * WPB + wave;
   const int32_t len = P.kv_lens[seq];
   const int32_t start = split * P.tokens_per_split;
   if (start >= len) return;  // the combine kernel never reads this split
@@ -145,220 +288,175 @@ __global__ __launch_bounds__(k_threads, 2) void decode_kernel(decode_params P) {
   const int32_t n_pages = (end - 1) / bt - first_page + 1;
 
   const uint16_t *table = P.tables + static_cast<uint64_t>(seq) * P.table_stride;
-  for (int32_t i = tid; i < n_pages; i += k_threads) {
+  int bad = 0;
+  for (int32_t i = tid; i < n_pages; i += NT) {
     const int32_t lb = first_page + i;
     const uint32_t page = lb < P.table_stride ? table[lb] : 0xFFFFFFFFu;
-    s_pages[i] = page < static_cast<uint32_t>(P.L.max_blocks) ? page : 0xFFFFFFFFu;
+    const bool ok = page < static_cast<uint32_t>(P.L.max_blocks);
+    s_pages[i] = ok ? page : 0xFFFFFFFFu;
+    bad |= ok ? 0 : 1;
   }
+  const bool clean = __syncthreads_or(bad) == 0;
 
-  const int32_t lane_in_row = tid % LPT;
-  const int32_t grp = tid / LPT;
-  const int32_t dim0 = lane_in_row * 16;
-  const uint64_t layer_base = static_cast<uint64_t>(P.layer) * P.L.layer_bytes +
-                              static_cast<uint64_t>(kvh) * P.L.region_bytes;
+  const int32_t lane_in_row = lane % LPT;
+  const int32_t grp = lane / LPT;
+  const uint8_t *k_base = P.k_pool + static_cast<uint64_t>(P.layer) * P.L.layer_bytes +
+                          static_cast<uint64_t>(kvh) * P.L.region_bytes;
+  const uint8_t *v_base = P.v_pool + static_cast<uint64_t>(P.layer) * P.L.layer_bytes +
+                          static_cast<uint64_t>(kvh) * P.L.region_bytes;
+  const uint64_t page_bytes = P.L.page_bytes;
 
-  // q for the G heads of this KV head, rounded to fp16.
-  half2_t qh[G][8];
+  decode_state<D, G, Q8> S;
 #pragma unroll
   for (int h = 0; h < G; ++h) {
-    const float *qp = P.q + (static_cast<uint64_t>(seq) * P.L.n_head + kvh * G + h) * D + dim0;
+    const float *qp = P.q + (static_cast<uint64_t>(seq) * P.L.n_head + kvh * G + h) * D;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const float4_t f = reinterpret_cast<const float4_t *>(qp)[j];
-      qh[h][2 * j] = pack_half2(f.x, f.y);
-      qh[h][2 * j + 1] = pack_half2(f.z, f.w);
+      const float4_t f =
+          *reinterpret_cast<const float4_t *>(qp + lane_dim<D, Q8>(lane_in_row, 4 * j));
+      S.qh[h][2 * j] = pack_half2(f.x, f.y);
+      S.qh[h][2 * j + 1] = pack_half2(f.z, f.w);
     }
+    S.m[h] = -INFINITY;
+    S.l[h] = 0.0f;
+    S.corr[h] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) S.acc[h][i] = 0.0f;
   }
 
-  float m[G], l[G], acc[G][16];
-#pragma unroll
-  for (int h = 0; h < G; ++h) {
-    m[h] = -INFINITY;
-    l[h] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) acc[h][i] = 0.0f;
-  }
-  __syncthreads();
-
-  // Byte offset of the page holding token `tok` (tok already clamped into
-  // the split by the caller).  Invalid pages read page 0 and are masked.
-  auto page_off = [&](int32_t tok, bool &ok) -> uint64_t {
-    const uint32_t page = s_pages[tok / bt - first_page];
-    const bool valid = page != 0xFFFFFFFFu;
-    ok = ok && valid;
-    return layer_base + static_cast<uint64_t>(valid ? page : 0u) * P.L.page_bytes;
-  };
-  auto load_pair = [&](int32_t tbase, bool &okA, bool &okB, row_regs<D, Q8> &ka,
-                       row_regs<D, Q8> &kb, row_regs<D, Q8> &va, row_regs<D, Q8> &vb) {
-    okA = tbase + grp < end;
-    okB = tbase + grp + NG < end;
-    const int32_t t0 = okA ? tbase + grp : start;
-    const int32_t t1 = okB ? tbase + grp + NG : start;
-    const uint64_t r0 = page_off(t0, okA);
-    const uint64_t r1 = page_off(t1, okB);
-    load_row<D, Q8>(P.k_pool + r0, t0 % bt, dim0, bt, ka);
-    load_row<D, Q8>(P.k_pool + r1, t1 % bt, dim0, bt, kb);
-    load_row<D, Q8>(P.v_pool + r0, t0 % bt, dim0, bt, va);
-    load_row<D, Q8>(P.v_pool + r1, t1 % bt, dim0, bt, vb);
-  };
-
-  row_regs<D, Q8> k0, k1, v0, v1;
-  bool ok0, ok1;
-  load_pair(start, ok0, ok1, k0, k1, v0, v1);
-
-  for (int32_t base = start; base < end; base += TT) {
-    // prefetch the next tile
-    const int32_t nbase = base + TT;
-    row_regs<D, Q8> nk0, nk1, nv0, nv1;
-    bool nok0 = false, nok1 = false;
-    if (nbase < end) load_pair(nbase, nok0, nok1, nk0, nk1, nv0, nv1);
-
-    // scores
-    half2_t kh0[8], kh1[8];
-    float ks0, ks1;
-    to_half<D, Q8>(k0, kh0, ks0);
-    to_half<D, Q8>(k1, kh1, ks1);
-    float s0[G], s1[G];
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      float a = 0.0f, b = 0.0f;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        a = dot2(qh[h][j], kh0[j], a);
-        b = dot2(qh[h][j], kh1[j], b);
-      }
-      if constexpr (Q8) {
-        a *= ks0;
-        b *= ks1;
-      }
-      s0[h] = group_sum<LPT>(a);
-      s1[h] = group_sum<LPT>(b);
-    }
-
-    // P.V.  f16 pools: V values of the two tokens paired per dimension and
-    // contracted with the fp16 pair (p0, p1) by v_dot2_f32_f16.  q8_0 pools:
-    // the int8 values are exact in fp32 and the per-token scale folds into
-    // an fp32 weight p*d_v, so nothing is rounded to fp16 (an fp16 p*d_v
-    // would cost up to ~2^-11 * 127 * d_v per dominant token).
-    [[maybe_unused]] half2_t vlo[8], vhi[8];
-    [[maybe_unused]] float vf0[16], vf1[16];
-    [[maybe_unused]] float vs0 = 1.0f, vs1 = 1.0f;
-    if constexpr (!Q8) {
-      half2_t vh0[8], vh1[8];
-      to_half<D, Q8>(v0, vh0, vs0);
-      to_half<D, Q8>(v1, vh1, vs1);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        vlo[j] = as_half2(__builtin_amdgcn_perm(as_u32(vh1[j]), as_u32(vh0[j]), 0x05040100u));
-        vhi[j] = as_half2(__builtin_amdgcn_perm(as_u32(vh1[j]), as_u32(vh0[j]), 0x07060302u));
-      }
+  // Loads the tile at `tbase` (rows past `end` and rows on invalid pages
+  // read a valid clamped address and are reported in ok0/ok1).
+  auto load_tile = [&](int32_t tbase, tile_regs<D, Q8> &T, bool &ok0, bool &ok1) {
+    if constexpr (UNIFORM) {
+      const int32_t ta = tbase;        // first token of half 0 (multiple of NGW)
+      const int32_t tb = tbase + NGW;  // first token of half 1
+      const bool hb = tb < end;
+      const uint32_t pa = __builtin_amdgcn_readfirstlane(s_pages[ta / bt - first_page]);
+      const uint32_t pb =
+          hb ? __builtin_amdgcn_readfirstlane(s_pages[tb / bt - first_page]) : pa;
+      const bool va = pa != 0xFFFFFFFFu;
+      const bool vb = pb != 0xFFFFFFFFu && hb;
+      const int32_t offa = ta % bt + grp;
+      const int32_t offb = (hb ? tb % bt : ta % bt) + grp;
+      ok0 = va && ta + grp < end;
+      ok1 = vb && tb + grp < end;
+      const uint64_t ra = static_cast<uint64_t>(va ? pa : 0u) * page_bytes;
+      const uint64_t rb = static_cast<uint64_t>(pb != 0xFFFFFFFFu ? pb : 0u) * page_bytes;
+      load_row<D, Q8>(k_base + ra, offa, lane_in_row, bt, T.k0);
+      load_row<D, Q8>(k_base + rb, offb, lane_in_row, bt, T.k1);
+      load_row<D, Q8>(v_base + ra, offa, lane_in_row, bt, T.v0);
+      load_row<D, Q8>(v_base + rb, offb, lane_in_row, bt, T.v1);
     } else {
-      i8x16_to_float(v0.a, vf0);
-      i8x16_to_float(v1.a, vf1);
-      vs0 = f16_bits_to_f32(static_cast<uint16_t>(v0.d));
-      vs1 = f16_bits_to_f32(static_cast<uint16_t>(v1.d));
+      const int32_t t0r = tbase + grp;
+      const int32_t t1r = tbase + grp + NGW;
+      const int32_t t0 = t0r < end ? t0r : start;
+      const int32_t t1 = t1r < end ? t1r : start;
+      const uint32_t p0 = s_pages[t0 / bt - first_page];
+      const uint32_t p1 = s_pages[t1 / bt - first_page];
+      ok0 = t0r < end && p0 != 0xFFFFFFFFu;
+      ok1 = t1r < end && p1 != 0xFFFFFFFFu;
+      const uint64_t r0 = static_cast<uint64_t>(p0 != 0xFFFFFFFFu ? p0 : 0u) * page_bytes;
+      const uint64_t r1 = static_cast<uint64_t>(p1 != 0xFFFFFFFFu ? p1 : 0u) * page_bytes;
+      load_row<D, Q8>(k_base + r0, t0 % bt, lane_in_row, bt, T.k0);
+      load_row<D, Q8>(k_base + r1, t1 % bt, lane_in_row, bt, T.k1);
+      load_row<D, Q8>(v_base + r0, t0 % bt, lane_in_row, bt, T.v0);
+      load_row<D, Q8>(v_base + r1, t1 % bt, lane_in_row, bt, T.v1);
     }
+  };
 
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      const float x0 = ok0 ? s0[h] : -INFINITY;
-      const float x1 = ok1 ? s1[h] : -INFINITY;
-      const float mn = fmaxf(m[h], fmaxf(x0, x1));
-      const float ms = mn == -INFINITY ? 0.0f : mn;
-      const float alpha = fast_exp2((m[h] - ms) * P.c);
-      const float p0 = fast_exp2((x0 - ms) * P.c);
-      const float p1 = fast_exp2((x1 - ms) * P.c);
-      l[h] = l[h] * alpha + (p0 + p1);
-      m[h] = mn;
-      if (alpha != 1.0f) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) acc[h][i] *= alpha;
-      }
-      if constexpr (Q8) {
-        const float w0 = p0 * vs0;
-        const float w1 = p1 * vs1;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) acc[h][i] = fmaf(w1, vf1[i], fmaf(w0, vf0[i], acc[h][i]));
-      } else {
-        const half2_t pp = pack_half2(p0, p1);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          acc[h][2 * j] = dot2(pp, vlo[j], acc[h][2 * j]);
-          acc[h][2 * j + 1] = dot2(pp, vhi[j], acc[h][2 * j + 1]);
-        }
-      }
+  // Full tiles of a split whose pages are all valid need no masks: they run
+  // unmasked through two register sets used alternately by code position
+  // (A, B, A, ...), so the next tile's loads stay in flight while the
+  // current one is consumed.  (Rotating one set into another with moves
+  // would force a wait for the in-flight loads.)  The split's partial last
+  // tile, and every tile of a split with an invalid page, run masked after.
+  const int32_t n_full = clean ? (end - start) / TT : 0;
+  int32_t base = start;
+  if (n_full > 0) {
+    // Loads are unconditional (a load past the last full tile re-reads the
+    // split's first tile and is discarded): no branch around them, so the
+    // compiler's wait counters can keep them in flight across the consume.
+    const int32_t last_full = start + (n_full - 1) * TT;
+    tile_regs<D, Q8> A, B;
+    bool u0, u1;
+    load_tile(base, A, u0, u1);
+    for (int32_t i = 0; i + 1 < n_full; i += 2) {
+      load_tile(base + TT, B, u0, u1);
+      consume_tile<D, G, Q8, false>(S, A, true, true, P.c);
+      base += TT;
+      const int32_t nb = base + TT <= last_full ? base + TT : start;
+      load_tile(nb, A, u0, u1);
+      consume_tile<D, G, Q8, false>(S, B, true, true, P.c);
+      base += TT;
     }
-
-    k0 = nk0;
-    k1 = nk1;
-    v0 = nv0;
-    v1 = nv1;
-    ok0 = nok0;
-    ok1 = nok1;
+    if (n_full & 1) {
+      consume_tile<D, G, Q8, false>(S, A, true, true, P.c);
+      base += TT;
+    }
+  }
+  for (; base < end; base += TT) {
+    tile_regs<D, Q8> T;
+    bool o0, o1;
+    load_tile(base, T, o0, o1);
+    consume_tile<D, G, Q8, true>(S, T, o0, o1, P.c);
   }
 
-  // merge the token groups of each wave (lane bits >= log2(LPT))
+  if constexpr (Q8) {
+    // acc holds sum w * (q + 128): remove the bias term
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) S.acc[h][i] = fmaf(-128.0f, S.corr[h], S.acc[h][i]);
+    }
+  }
+
+  // merge the token groups of the wave (lane bits >= log2(LPT))
 #pragma unroll
   for (int mask = LPT; mask < k_wave; mask <<= 1) {
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-      const float mo = wave_shfl_xor(m[h], mask);
-      const float lo = wave_shfl_xor(l[h], mask);
-      const float mn = fmaxf(m[h], mo);
+      const float mo = wave_shfl_xor(S.m[h], mask);
+      const float lo = wave_shfl_xor(S.l[h], mask);
+      const float mn = fmaxf(S.m[h], mo);
       const float ms = mn == -INFINITY ? 0.0f : mn;
-      const float a = fast_exp2((m[h] - ms) * P.c);
-      const float b = fast_exp2((mo - ms) * P.c);
-      l[h] = l[h] * a + lo * b;
+      const float a = fast_exp2(S.m[h] - ms);
+      const float b = fast_exp2(mo - ms);
+      S.l[h] = S.l[h] * a + lo * b;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) acc[h][i] = acc[h][i] * a + wave_shfl_xor(acc[h][i], mask) * b;
-      m[h] = mn;
+      for (int i = 0; i < 16; ++i) {
+        S.acc[h][i] = S.acc[h][i] * a + wave_shfl_xor(S.acc[h][i], mask) * b;
+      }
+      S.m[h] = mn;
     }
   }
-  const int32_t wave = tid / k_wave;
-  if ((tid % k_wave) < LPT) {
+  if (grp == 0) {
 #pragma unroll
     for (int h = 0; h < G; ++h) {
+      const uint64_t slot =
+          (static_cast<uint64_t>(seq) * P.L.n_head + kvh * G + h) * P.max_splits + split;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) s_acc[wave][h][dim0 + i] = acc[h][i];
-      if (lane_in_row == 0) {
-        s_ml[wave][h][0] = m[h];
-        s_ml[wave][h][1] = l[h];
+      for (int j = 0; j < 4; ++j) {
+        *reinterpret_cast<float4_t *>(P.part_acc + slot * D +
+                                      lane_dim<D, Q8>(lane_in_row, 4 * j)) =
+            float4_t{S.acc[h][4 * j], S.acc[h][4 * j + 1], S.acc[h][4 * j + 2],
+                     S.acc[h][4 * j + 3]};
       }
-    }
-  }
-  __syncthreads();
-  for (int32_t idx = tid; idx < G * D; idx += k_threads) {
-    const int32_t h = idx / D;
-    const int32_t d = idx % D;
-    float mx = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < k_waves; ++w) mx = fmaxf(mx, s_ml[w][h][0]);
-    const float ms = mx == -INFINITY ? 0.0f : mx;
-    float lsum = 0.0f, asum = 0.0f;
-#pragma unroll
-    for (int w = 0; w < k_waves; ++w) {
-      const float f = fast_exp2((s_ml[w][h][0] - ms) * P.c);
-      lsum += s_ml[w][h][1] * f;
-      asum += s_acc[w][h][d] * f;
-    }
-    const uint64_t slot =
-        (static_cast<uint64_t>(seq) * P.L.n_head + kvh * G + h) * P.max_splits + split;
-    P.part_acc[slot * D + d] = asum;
-    if (d == 0) {
-      P.part_ml[slot * 2] = mx;
-      P.part_ml[slot * 2 + 1] = lsum;
+      if (lane_in_row == 0) {
+        P.part_ml[slot * 2] = S.m[h];
+        P.part_ml[slot * 2 + 1] = S.l[h];
+      }
     }
   }
 }
 
-// Merges the split partials of one (sequence, head): o = sum_s e^{m_s-M} acc_s
-// / sum_s e^{m_s-M} l_s.
+// Merges the split partials of one (sequence, head): o = sum_s 2^{m_s-M} acc_s
+// / sum_s 2^{m_s-M} l_s (m in the log2 domain, scale folded in).
 template <int D>
 __global__ __launch_bounds__(D) void combine_kernel(const float *__restrict__ part_acc,
                                                      const float *__restrict__ part_ml,
                                                      const int32_t *__restrict__ kv_lens,
                                                      int32_t n_head, int32_t max_splits,
-                                                     int32_t tokens_per_split, float c,
+                                                     int32_t tokens_per_split,
                                                      float *__restrict__ out) {
   const int32_t row = blockIdx.x;  // seq * n_head + head
   const int32_t seq = row / n_head;
@@ -372,7 +470,7 @@ __global__ __launch_bounds__(D) void combine_kernel(const float *__restrict__ pa
   const float ms = mx == -INFINITY ? 0.0f : mx;
   float lsum = 0.0f, asum = 0.0f;
   for (int32_t s = 0; s < n; ++s) {
-    const float f = fast_exp2((ml[2 * s] - ms) * c);
+    const float f = fast_exp2(ml[2 * s] - ms);
     lsum += ml[2 * s + 1] * f;
     asum += pa[static_cast<uint64_t>(s) * D + d] * f;
   }
@@ -392,14 +490,31 @@ int32_t env_int(const char *name, int32_t fallback) {
   return x > 0 ? static_cast<int32_t>(x) : fallback;
 }
 
+// Compute units of the current device (cached per device id).
+int32_t device_cu_count() {
+  static int32_t cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0) {
+      cus = 256;
+    }
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
 // Split sizing: enough workgroups to cover 256 CUs several times over, each
 // split a whole number of tiles, and its page list within the LDS cache.
 decode_plan plan_decode(const pool_layout &L, int32_t n_seq, int32_t max_kv_len) {
   decode_plan p;
   const int32_t lpt = L.head_dim / 16;
-  const int32_t tile = 2 * (k_threads / lpt);
-  const int32_t units = n_seq * L.n_head_kv;
-  const int32_t target = env_int("EMELK_DECODE_TARGET_WG", 2048);
+  const int32_t tile = 2 * (k_wave / lpt);
+  const int32_t wpb = waves_per_block(L.n_head_kv);
+  const int32_t units = n_seq * (L.n_head_kv / wpb);
+  const int32_t target = env_int("EMELK_DECODE_TARGET_WG", device_cu_count());
   const int32_t tiles = (max_kv_len + tile - 1) / tile;
   int32_t splits = (target + units - 1) / units;
   splits = splits < 1 ? 1 : (splits > tiles ? tiles : splits);
@@ -416,9 +531,25 @@ decode_plan plan_decode(const pool_layout &L, int32_t n_seq, int32_t max_kv_len)
   return p;
 }
 
+template <int D, int G, bool Q8, int WPB>
+void launch_decode_wpb(const decode_params &P, dim3 grid, hipStream_t st) {
+  constexpr int NGW = k_wave / (D / 16);
+  if (P.L.block_tokens % NGW == 0) {
+    hipLaunchKernelGGL((decode_kernel<D, G, Q8, true, WPB>), grid, dim3(WPB * k_wave), 0, st, P);
+  } else {
+    hipLaunchKernelGGL((decode_kernel<D, G, Q8, false, WPB>), grid, dim3(WPB * k_wave), 0, st,
+                       P);
+  }
+}
+
 template <int D, int G, bool Q8>
 void launch_decode(const decode_params &P, dim3 grid, hipStream_t st) {
-  hipLaunchKernelGGL((decode_kernel<D, G, Q8>), grid, dim3(k_threads), 0, st, P);
+  switch (waves_per_block(P.L.n_head_kv)) {
+    case 8: launch_decode_wpb<D, G, Q8, 8>(P, grid, st); break;
+    case 4: launch_decode_wpb<D, G, Q8, 4>(P, grid, st); break;
+    case 2: launch_decode_wpb<D, G, Q8, 2>(P, grid, st); break;
+    default: launch_decode_wpb<D, G, Q8, 1>(P, grid, st); break;
+  }
 }
 
 template <int D, bool Q8>
@@ -477,7 +608,7 @@ extern "C" emel_error_type emelk_attn_decode(const emelk_kv_geometry *g, const v
   const uint64_t acc_floats = static_cast<uint64_t>(n_seq) * L.n_head * plan.max_splits * L.head_dim;
   P.part_acc = static_cast<float *>(workspace);
   P.part_ml = P.part_acc + acc_floats;
-  const dim3 grid(plan.max_splits, L.n_head_kv, n_seq);
+  const dim3 grid(plan.max_splits, L.n_head_kv / emelk::waves_per_block(L.n_head_kv), n_seq);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int32_t group = L.n_head / L.n_head_kv;
   const bool q8 = L.kv_type == EMELK_KV_Q8_0;
@@ -493,10 +624,10 @@ extern "C" emel_error_type emelk_attn_decode(const emelk_kv_geometry *g, const v
   const dim3 cgrid(n_seq * L.n_head);
   if (L.head_dim == 128) {
     hipLaunchKernelGGL(emelk::combine_kernel<128>, cgrid, dim3(128), 0, st, P.part_acc, P.part_ml,
-                       kv_lens, L.n_head, plan.max_splits, plan.tokens_per_split, P.c, out);
+                       kv_lens, L.n_head, plan.max_splits, plan.tokens_per_split, out);
   } else {
     hipLaunchKernelGGL(emelk::combine_kernel<64>, cgrid, dim3(64), 0, st, P.part_acc, P.part_ml,
-                       kv_lens, L.n_head, plan.max_splits, plan.tokens_per_split, P.c, out);
+                       kv_lens, L.n_head, plan.max_splits, plan.tokens_per_split, out);
   }
   return hipGetLastError() == hipSuccess ? EMELK_ERR_NONE : EMELK_ERR_BACKEND;
 }
