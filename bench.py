@@ -34,6 +34,13 @@ sys.path.insert(0, os.path.join(ROOT, "emel.cpp_amd"))
 
 HBM_PEAK_GBS = 8000.0
 
+# HBM bytes per decode_kernel launch on the default workload, from the two
+# rocprofv3 PMC runs (FETCH_SIZE, WRITE_SIZE) summarised in
+# profiles/decode_kernel_llama3-8b-b64-ctx8k.md, each scaled by the same
+# counter's reading on a plain 1 GiB copy (bench.py --copy-calibration):
+# FETCH_SIZE x2.000, WRITE_SIZE x1.000.
+PMC_TRAFFIC_BYTES = {"llama3-8b-b64-ctx8k": 2158627371}
+
 CONFIGS = {
     # name: (n_layer, n_head, n_kv, head_dim, block_tokens, batch, ctx, kv_type)
     "llama3-8b-b64-ctx8k": (32, 32, 8, 128, 32, 64, 8192, "f16"),
@@ -57,6 +64,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only copy 1 GiB device-to-device three times (the reference kernel "
+                         "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the KV hot path shards by "
@@ -64,9 +74,18 @@ def main():
         sys.exit(2)
 
     import torch
-    import emelk
 
     dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        a = torch.ones(1 << 30, dtype=torch.uint8, device=dev)
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": 1 << 30, "copies": 3}))
+        return
+    import emelk
+
     if args.config == "llama3-8b-prefill512-evict25":
         return prefill_evict(args, torch, emelk, dev)
     L, H, HK, D, BT, B, CTX, kvt = CONFIGS[args.config]
@@ -241,7 +260,8 @@ def main():
                    "ctx": int(ctx[0]) if CTX else "U[1024,4096]", "kv": kvt,
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": PMC_TRAFFIC_BYTES.get(args.config),
                      "kernel": "decode_kernel + combine_kernel (HIP events per layer call)",
                      "bytes_per_launch": kernel_bytes, "avg_launch_ms": round(attn_avg_ms, 4)},
         "cpu_baseline": cpu,

@@ -506,8 +506,11 @@ int32_t device_cu_count() {
   return cached[dev];
 }
 
-// Split sizing: enough workgroups to cover 256 CUs several times over, each
-// split a whole number of tiles, and its page list within the LDS cache.
+// Split sizing: about one workgroup per CU (a workgroup is 8 waves, which is
+// what one CU holds at this kernel's register budget; more, shorter splits
+// measured slower because every split pays its page-list load and merge),
+// each split a whole number of wave tiles with its page list inside the LDS
+// cache.
 decode_plan plan_decode(const pool_layout &L, int32_t n_seq, int32_t max_kv_len) {
   decode_plan p;
   const int32_t lpt = L.head_dim / 16;
