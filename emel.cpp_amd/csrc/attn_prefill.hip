@@ -5,9 +5,9 @@
 // attends causally to logical positions [0, q_start + r]) with one flash
 // attention pass per chunk.
 //
-// Workgroup = 4 waves = one KV head, G_WG query heads of its group and RB
-// row blocks of 32 query rows (G_WG * RB = 4), so the four waves share every
-// K/V tile staged in LDS.  Per 32-key tile each wave computes
+// Workgroup = 8 waves = one KV head, G_WG query heads of its group and RB
+// row blocks of 32 query rows (G_WG * RB = 8), so the eight waves share
+// every K/V tile staged in LDS (256 flops per staged byte at D = 128).  Per 32-key tile each wave computes
 //     S^T (32 keys x 32 rows)  = K (32 x D) . Q^T (D x 32)      D/16 MFMAs
 // so a lane holds 16 of the 32 scores of ONE query row (the other 16 sit in
 // the lane 32 apart): the row max and sum are in-lane plus one cross-half
@@ -34,8 +34,9 @@ namespace {
 
 using namespace emelk::dev;
 
-constexpr int k_threads = 256;
 constexpr int k_tile = 32;  // keys per tile
+constexpr float k_rescale = 8.0f;  // lazy-rescale threshold (log2 units)
+constexpr int k_max_seq_pages = EMELK_MAX_BLOCKS_PER_SEQUENCE;  // LDS page list
 
 typedef _Float16 half8_v __attribute__((ext_vector_type(8)));
 typedef float float16_v __attribute__((ext_vector_type(16)));
@@ -52,6 +53,7 @@ struct prefill_params {
   const uint16_t *tables;
   int32_t table_stride;
   float c;  // scale * log2(e)
+  int32_t bt_shift;  // log2(block_tokens) when a power of two, else -1
 };
 
 // Slot of key k (0..31) in the MFMA k-order of the score accumulator:
@@ -67,41 +69,55 @@ __device__ __forceinline__ int key_slot(int k) {
 }
 
 template <int D, int G_WG, int RB>
-__global__ __launch_bounds__(k_threads) void prefill_kernel(prefill_params P) {
-  static_assert(G_WG * RB == 4, "four waves per workgroup");
+__global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_params P) {
+  constexpr int WAVES = G_WG * RB;
+  constexpr int NT = WAVES * k_wave;
   constexpr int KSTEPS = D / 16;   // MFMA k-steps for S^T
   constexpr int DCH = D / 32;      // 32-wide dim chunks of O
   constexpr int KROW = D + 8;      // padded LDS row (halves) of K
   constexpr int VROW = k_tile + 8; // padded LDS row (halves) of V^T
-  constexpr int PARTS = k_threads / k_tile;  // staging threads per key row (8)
-  constexpr int PW = D / PARTS;              // dims per staging thread (16 or 8)
-  constexpr int NL = PW / 8;                 // 16-byte loads per row part
+  constexpr int PARTS = NT / k_tile;         // staging threads per key row
+  constexpr int PW = D / PARTS;              // dims per staging thread
+  static_assert(PW == 8 || PW == 4, "K staging chunk is 16 or 8 bytes");
 
   __shared__ half_t s_k[2][k_tile][KROW];
   __shared__ half_t s_vt[2][D][VROW];
-  __shared__ float s_row[4][32];
+  __shared__ float s_row[WAVES][32];
+  __shared__ uint32_t s_ptab[k_max_seq_pages];
+
+  // Workgroup -> (query tile, head group, sequence).  Consecutive workgroup
+  // ids are spread over the 8 XCDs; the mapping gives each XCD a contiguous
+  // run of (head group, sequence) units with all their query tiles, so the
+  // tiles that re-read one unit's K/V share that XCD's L2.
+  const int n_qt = (P.n_q + RB * 32 - 1) / (RB * 32);
+  const int n_hg = P.L.n_head / G_WG;
+  const int total_wg = gridDim.x;
+  int lin = blockIdx.x;
+  if ((total_wg & 7) == 0) lin = (blockIdx.x >> 3) + (total_wg >> 3) * (blockIdx.x & 7);
+  const int qt = lin % n_qt;
+  const int hg = (lin / n_qt) % n_hg;
+  const int seq = lin / (n_qt * n_hg);
 
   const int tid = threadIdx.x;
   const int wave = tid / k_wave;
   const int lane = tid % k_wave;
   const int h = lane / 32;
   const int l32 = lane % 32;
-  const int seq = blockIdx.z;
   const int group = P.L.n_head / P.L.n_head_kv;
-  const int head0 = blockIdx.y * G_WG;
+  const int head0 = hg * G_WG;
   const int kvh = head0 / group;
   const int head = head0 + wave % G_WG;
-  const int row0 = (blockIdx.x * RB + wave / G_WG) * 32;
+  const int row0 = (qt * RB + wave / G_WG) * 32;
   const int n_q = P.n_q;
   const int q0 = P.q_start[seq];
   const int total = q0 + n_q;
-  const int wg_row_end = min(n_q, (blockIdx.x + 1) * RB * 32);
-  if (blockIdx.x * RB * 32 >= n_q) return;
+  const int wg_row_end = min(n_q, (qt + 1) * RB * 32);
   const int key_end = q0 + wg_row_end;  // exclusive
   const int n_tiles = (key_end + k_tile - 1) / k_tile;
   const int my_row = row0 + l32;
   const bool row_ok = my_row < n_q;
   const int my_pos = q0 + my_row;
+  const int wg_first_pos = q0 + qt * RB * 32;  // smallest query position in the WG
 
   // Q^T operand (B): lane holds query my_row, dims 16*kk + 8*h .. +7.
   half8_v qop[KSTEPS];
@@ -137,52 +153,100 @@ __global__ __launch_bounds__(k_threads) void prefill_kernel(prefill_params P) {
   const uint64_t layer_base = static_cast<uint64_t>(P.layer) * P.L.layer_bytes +
                               static_cast<uint64_t>(kvh) * P.L.region_bytes;
   const uint16_t *table = P.tables + static_cast<uint64_t>(seq) * P.table_stride;
-  uint4_t rk[2], rv[2];
+  {
+    const int n_pages = min((key_end + P.L.block_tokens - 1) / P.L.block_tokens,
+                            k_max_seq_pages);
+    for (int i = tid; i < n_pages; i += NT) {
+      const uint32_t page = i < P.table_stride ? table[i] : 0xFFFFFFFFu;
+      s_ptab[i] = page < static_cast<uint32_t>(P.L.max_blocks) ? page : 0xFFFFFFFFu;
+    }
+    __syncthreads();
+  }
+  // K staging: thread -> one PW-dim chunk (16 or 8 bytes) of one key row.
+  // V staging at D = 128: thread -> 4 consecutive keys x 2 dims (lane-fast
+  // dims keep each key row coalesced), transposed in registers so each
+  // dim's 4 keys reach LDS as one 8-byte store in the accumulator's key
+  // order.  D = 64: one key x PW dims, stored element-wise.
+  constexpr bool VT4 = (D == 128);
+  const int vt_dp = tid % (D / 2);       // dim pair
+  const int vt_kg = tid / (D / 2);       // key group (4 keys)
+  struct stage_t {
+    uint4_t rk16;
+    uint2 rk8, rv8;
+    uint32_t rv4[4];
+  };
 
-  auto load_tile = [&](int t) {
-    const int key = t * k_tile + st_key;
-    const int lb = key / P.L.block_tokens;
-    uint32_t page = 0xFFFFFFFFu;
-    if (key < total && lb < P.table_stride) page = table[lb];
+  // Page of a key from the LDS copy of this sequence's page list (no
+  // dependent global load between a tile's address and its data).
+  const int bt = P.L.block_tokens;
+  const int bt_shift = P.bt_shift;  // log2(block_tokens), or -1
+  auto key_offset = [&](int key, uint32_t &ok) -> uint64_t {
+    const int lb = bt_shift >= 0 ? key >> bt_shift : key / bt;
+    const int row = bt_shift >= 0 ? key & (bt - 1) : key % bt;
+    // a sequence holds at most k_max_seq_pages pages (MAX_BLOCKS_PER_SEQUENCE)
+    const uint32_t page = (key < total && lb < k_max_seq_pages) ? s_ptab[lb] : 0xFFFFFFFFu;
+    ok = page != 0xFFFFFFFFu ? 1u : 0u;
+    return layer_base + static_cast<uint64_t>(ok ? page : 0u) * P.L.page_bytes +
+           static_cast<uint64_t>(row) * D * 2u;
+  };
+  auto load_tile = [&](int t, stage_t &R) {
+    {
+      uint32_t ok;
+      const uint64_t off = key_offset(t * k_tile + st_key, ok) + st_part * PW * 2u;
+      if constexpr (PW == 8) {
+        R.rk16 = ok ? load16(P.k_pool + off) : uint4_t{0u, 0u, 0u, 0u};
+      } else {
+        R.rk8 = ok ? *reinterpret_cast<const uint2 *>(P.k_pool + off) : uint2{0u, 0u};
+        R.rv8 = ok ? *reinterpret_cast<const uint2 *>(P.v_pool + off) : uint2{0u, 0u};
+      }
+    }
+    if constexpr (VT4) {
+      // the 4 keys share a page whenever block_tokens is a multiple of 4
+      const int key0 = t * k_tile + 4 * vt_kg;
+      const bool same_page = (bt & 3) == 0;
+      uint32_t ok0;
+      const uint64_t off0 = key_offset(key0, ok0) + 4u * vt_dp;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) rk[j] = rv[j] = uint4_t{0u, 0u, 0u, 0u};
-    if (page < static_cast<uint32_t>(P.L.max_blocks)) {
-      const uint64_t off = layer_base + static_cast<uint64_t>(page) * P.L.page_bytes +
-                           (static_cast<uint64_t>(key % P.L.block_tokens) * D + st_part * PW) * 2u;
-#pragma unroll
-      for (int j = 0; j < NL; ++j) {
-        rk[j] = load16(P.k_pool + off + 16 * j);
-        rv[j] = load16(P.v_pool + off + 16 * j);
+      for (int j = 0; j < 4; ++j) {
+        uint32_t ok = ok0;
+        uint64_t off = off0 + static_cast<uint64_t>(j) * D * 2u;
+        if (!same_page) off = key_offset(key0 + j, ok) + 4u * vt_dp;
+        ok = ok && (key0 + j < total);
+        R.rv4[j] = ok ? *reinterpret_cast<const uint32_t *>(P.v_pool + off) : 0u;
       }
     }
   };
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int j = 0; j < NL; ++j) {
-      *reinterpret_cast<uint4_t *>(&s_k[buf][st_key][st_part * PW + 8 * j]) = rk[j];
+  auto store_tile = [&](int buf, const stage_t &R) {
+    if constexpr (PW == 8) {
+      *reinterpret_cast<uint4_t *>(&s_k[buf][st_key][st_part * PW]) = R.rk16;
+    } else {
+      *reinterpret_cast<uint2 *>(&s_k[buf][st_key][st_part * PW]) = R.rk8;
     }
-    const int slot = key_slot(st_key);
+    if constexpr (VT4) {
+      if (vt_kg < k_tile / 4) {
+        const int slot = key_slot(4 * vt_kg);  // 4 consecutive keys -> 4 consecutive slots
+        const uint32_t lo01 = __builtin_amdgcn_perm(R.rv4[1], R.rv4[0], 0x05040100u);
+        const uint32_t lo23 = __builtin_amdgcn_perm(R.rv4[3], R.rv4[2], 0x05040100u);
+        const uint32_t hi01 = __builtin_amdgcn_perm(R.rv4[1], R.rv4[0], 0x07060302u);
+        const uint32_t hi23 = __builtin_amdgcn_perm(R.rv4[3], R.rv4[2], 0x07060302u);
+        *reinterpret_cast<uint2 *>(&s_vt[buf][2 * vt_dp][slot]) = uint2{lo01, lo23};
+        *reinterpret_cast<uint2 *>(&s_vt[buf][2 * vt_dp + 1][slot]) = uint2{hi01, hi23};
+      }
+    } else {
+      const int slot = key_slot(st_key);
+      const uint32_t w[2] = {R.rv8.x, R.rv8.y};
 #pragma unroll
-    for (int j = 0; j < NL; ++j) {
-      const uint32_t w[4] = {rv[j].x, rv[j].y, rv[j].z, rv[j].w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int dim = st_part * PW + 8 * j + 2 * e;
+      for (int e = 0; e < 2; ++e) {
+        const int dim = st_part * PW + 2 * e;
         s_vt[buf][dim][slot] = __builtin_bit_cast(half_t, static_cast<uint16_t>(w[e] & 0xFFFFu));
         s_vt[buf][dim + 1][slot] = __builtin_bit_cast(half_t, static_cast<uint16_t>(w[e] >> 16));
       }
     }
   };
 
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
-
-  for (int t = 0; t < n_tiles; ++t) {
+  // One tile: scores, online softmax, O update, from LDS buffer t & 1.
+  auto compute = [&](int t) {
     const int buf = t & 1;
-    const bool more = t + 1 < n_tiles;
-    if (more) load_tile(t + 1);
-
     // S^T = K . Q^T
     float16_v s;
 #pragma unroll
@@ -193,47 +257,68 @@ __global__ __launch_bounds__(k_threads) void prefill_kernel(prefill_params P) {
       s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qop[kk], s, 0, 0, 0);
     }
 
-    // mask + online softmax for query my_row (in-lane 16 keys + other half)
+    // Online softmax for query my_row (16 keys in-lane + the other half).
+    // Only tiles reaching past the workgroup's first query position or the
+    // sequence end need the causal mask.
+    const int tile_last = t * k_tile + k_tile - 1;
     float tmax = -INFINITY;
+    if (tile_last <= wg_first_pos && tile_last < total) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int key = t * k_tile + 8 * (r / 4) + 4 * h + (r % 4);
-      const bool ok = row_ok && key <= my_pos && key < total;
-      s[r] = ok ? s[r] * P.c : -INFINITY;
-      tmax = fmaxf(tmax, s[r]);
+      for (int r = 0; r < 16; ++r) {
+        s[r] *= P.c;
+        tmax = fmaxf(tmax, s[r]);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = t * k_tile + 8 * (r / 4) + 4 * h + (r % 4);
+        const bool ok = key <= my_pos && key < total;
+        s[r] = ok ? s[r] * P.c : -INFINITY;
+        tmax = fmaxf(tmax, s[r]);
+      }
     }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, k_wave));
-    const float mn = fmaxf(m, tmax);
-    const float ms = mn == -INFINITY ? 0.0f : mn;
-    const float alpha = fast_exp2(m - ms);
+    // Lazy rescale: the reference max moves only when a score passes it by
+    // more than 2^8, so P <= 256 and the O rescale is skipped on almost
+    // every tile.
+    const bool need = tmax > m + k_rescale;
+    float alpha = 1.0f;
+    if (need) {
+      alpha = fast_exp2(m - tmax);  // 0 while the row had no valid key yet
+      l *= alpha;
+      m = tmax;
+    }
     float psum = 0.0f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      s[r] = fast_exp2(s[r] - ms);
+      const float pr = fast_exp2(s[r] - m);
+      s[r] = s[r] == -INFINITY ? 0.0f : pr;  // also covers m == -inf
       psum += s[r];
     }
     psum += __shfl_xor(psum, 32, k_wave);
-    l = l * alpha + psum;
-    m = mn;
+    l += psum;
 
-    // alpha of each O row: rows 8a + 4h + b live in lane (row), so pass them
-    // through LDS (wave-private slice)
-    if (h == 0) s_row[wave][l32] = alpha;
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the write lands before the reads
-    __builtin_amdgcn_wave_barrier();
-    float arow[16];
+    if (__builtin_amdgcn_ballot_w64(need) != 0) {
+      // alpha of each O row: rows 8a + 4h + b live in lane (row), so pass
+      // them through LDS (wave-private slice)
+      if (h == 0) s_row[wave][l32] = alpha;
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the write lands before the reads
+      __builtin_amdgcn_wave_barrier();
+      float arow[16];
 #pragma unroll
-    for (int a4 = 0; a4 < 4; ++a4) {
-      const float4_t v = *reinterpret_cast<const float4_t *>(&s_row[wave][8 * a4 + 4 * h]);
-      arow[4 * a4 + 0] = v.x;
-      arow[4 * a4 + 1] = v.y;
-      arow[4 * a4 + 2] = v.z;
-      arow[4 * a4 + 3] = v.w;
-    }
+      for (int a4 = 0; a4 < 4; ++a4) {
+        const float4_t v = *reinterpret_cast<const float4_t *>(&s_row[wave][8 * a4 + 4 * h]);
+        arow[4 * a4 + 0] = v.x;
+        arow[4 * a4 + 1] = v.y;
+        arow[4 * a4 + 2] = v.z;
+        arow[4 * a4 + 3] = v.w;
+      }
+      __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int c = 0; c < DCH; ++c) {
+      for (int c = 0; c < DCH; ++c) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) o[c][r] *= arow[r];
+        for (int r = 0; r < 16; ++r) o[c][r] *= arow[r];
+      }
     }
 
     // O += P . V
@@ -252,7 +337,21 @@ __global__ __launch_bounds__(k_threads) void prefill_kernel(prefill_params P) {
       }
     }
 
-    if (more) store_tile(buf ^ 1);
+  };
+
+  // Single register stage: tile t + 1 is loaded at the start of tile t and
+  // written to the other LDS buffer after tile t's MFMAs.  (Deeper register
+  // rings were measured slower: the unrolled copies cost registers the MFMA
+  // and softmax code needs at 8 waves per CU.)
+  stage_t R;
+  load_tile(0, R);
+  store_tile(0, R);
+  __syncthreads();
+  for (int t = 0; t < n_tiles; ++t) {
+    const bool more = t + 1 < n_tiles;
+    if (more) load_tile(t + 1, R);
+    compute(t);
+    if (more) store_tile((t + 1) & 1, R);
     __syncthreads();
   }
 
@@ -274,14 +373,18 @@ __global__ __launch_bounds__(k_threads) void prefill_kernel(prefill_params P) {
 
 template <int D>
 bool launch_prefill(const prefill_params &P, int32_t n_seq, hipStream_t st) {
+  // 8 waves per workgroup: G_WG query heads of one KV group x RB blocks of
+  // 32 query rows, all sharing each staged K/V tile.
   const int group = P.L.n_head / P.L.n_head_kv;
-  const int g_wg = group < 4 ? group : 4;
-  const int rb = 4 / g_wg;
-  const dim3 grid((P.n_q + 32 * rb - 1) / (32 * rb), P.L.n_head / g_wg, n_seq);
+  const int g_wg = group < 8 ? group : 8;
+  const int rb = 8 / g_wg;
+  const int n_qt = (P.n_q + 32 * rb - 1) / (32 * rb);
+  const dim3 grid(n_qt * (P.L.n_head / g_wg) * n_seq);
   switch (g_wg) {
-    case 1: hipLaunchKernelGGL((prefill_kernel<D, 1, 4>), grid, dim3(k_threads), 0, st, P); return true;
-    case 2: hipLaunchKernelGGL((prefill_kernel<D, 2, 2>), grid, dim3(k_threads), 0, st, P); return true;
-    case 4: hipLaunchKernelGGL((prefill_kernel<D, 4, 1>), grid, dim3(k_threads), 0, st, P); return true;
+    case 1: hipLaunchKernelGGL((prefill_kernel<D, 1, 8>), grid, dim3(512), 0, st, P); return true;
+    case 2: hipLaunchKernelGGL((prefill_kernel<D, 2, 4>), grid, dim3(512), 0, st, P); return true;
+    case 4: hipLaunchKernelGGL((prefill_kernel<D, 4, 2>), grid, dim3(512), 0, st, P); return true;
+    case 8: hipLaunchKernelGGL((prefill_kernel<D, 8, 1>), grid, dim3(512), 0, st, P); return true;
     default: return false;
   }
 }
@@ -316,6 +419,10 @@ extern "C" emel_error_type emelk_attn_prefill_chunk(const emelk_kv_geometry *g, 
   P.tables = block_tables;
   P.table_stride = table_stride;
   P.c = scale * 1.4426950408889634f;
+  P.bt_shift = -1;
+  for (int b = 0; b < 16; ++b) {
+    if ((1 << b) == L.block_tokens) P.bt_shift = b;
+  }
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool ok = L.head_dim == 128 ? emelk::launch_prefill<128>(P, n_seq, st)
                                     : emelk::launch_prefill<64>(P, n_seq, st);
