@@ -144,8 +144,9 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[c][r] = 0.0f;
   }
-  float m = -INFINITY;
+  float m = -INFINITY;  // raw-score reference max of this lane's row
   float l = 0.0f;
+  const float rescale_raw = k_rescale / P.c;
 
   // staging: thread -> (key, PW-dim part) of the 32-key tile
   const int st_part = tid % PARTS;
@@ -261,39 +262,47 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
     // Only tiles reaching past the workgroup's first query position or the
     // sequence end need the causal mask.
     const int tile_last = t * k_tile + k_tile - 1;
+    const bool interior = tile_last <= wg_first_pos && tile_last < total;
     float tmax = -INFINITY;
-    if (tile_last <= wg_first_pos && tile_last < total) {
+    if (interior) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        s[r] *= P.c;
-        tmax = fmaxf(tmax, s[r]);
-      }
+      for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[r]);
     } else {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int key = t * k_tile + 8 * (r / 4) + 4 * h + (r % 4);
         const bool ok = key <= my_pos && key < total;
-        s[r] = ok ? s[r] * P.c : -INFINITY;
+        s[r] = ok ? s[r] : -INFINITY;
         tmax = fmaxf(tmax, s[r]);
       }
     }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, k_wave));
-    // Lazy rescale: the reference max moves only when a score passes it by
-    // more than 2^8, so P <= 256 and the O rescale is skipped on almost
-    // every tile.
-    const bool need = tmax > m + k_rescale;
+    // Scores stay raw (q.k); p = exp2(s*c - m*c) is one FMA + exp2.  Lazy
+    // rescale: the reference max moves only when a score passes it by more
+    // than 2^8 after scaling, so P <= 256 and the O rescale is skipped on
+    // almost every tile.
+    const bool need = tmax > m + rescale_raw;
     float alpha = 1.0f;
     if (need) {
-      alpha = fast_exp2(m - tmax);  // 0 while the row had no valid key yet
+      alpha = fast_exp2((m - tmax) * P.c);  // 0 while the row had no valid key yet
       l *= alpha;
       m = tmax;
     }
+    const float mc = m * P.c;
     float psum = 0.0f;
+    if (interior) {  // every score finite, m finite
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float pr = fast_exp2(s[r] - m);
-      s[r] = s[r] == -INFINITY ? 0.0f : pr;  // also covers m == -inf
-      psum += s[r];
+      for (int r = 0; r < 16; ++r) {
+        s[r] = fast_exp2(fmaf(s[r], P.c, -mc));
+        psum += s[r];
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float pr = fast_exp2(fmaf(s[r], P.c, -mc));
+        s[r] = s[r] == -INFINITY ? 0.0f : pr;  // also covers m == -inf
+        psum += s[r];
+      }
     }
     psum += __shfl_xor(psum, 32, k_wave);
     l += psum;
@@ -340,9 +349,10 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
   };
 
   // Single register stage: tile t + 1 is loaded at the start of tile t and
-  // written to the other LDS buffer after tile t's MFMAs.  (Deeper register
-  // rings were measured slower: the unrolled copies cost registers the MFMA
-  // and softmax code needs at 8 waves per CU.)
+  // written to the other LDS buffer after tile t's MFMAs.  Deeper register
+  // rings, and a software pipeline issuing tile t+1's QK MFMAs before tile
+  // t's softmax, were both measured slower: their unrolled copies push the
+  // kernel past 256 registers per lane, the budget at 8 waves per CU.
   stage_t R;
   load_tile(0, R);
   store_tile(0, R);
