@@ -339,3 +339,83 @@ def test_prefill_chunk_edges(device):
     _prefill_case(device, 8, 4, 64, 16, [0, 33], 40, seed=32)
     _prefill_case(device, 4, 4, 128, 16, [5], 7, seed=33)
     _prefill_case(device, 16, 2, 128, 32, [64], 33, seed=34)  # G=8
+
+
+def test_decode_masks_invalid_pages_and_short_tables(device):
+    # Tokens on pages marked EMELK_INVALID_KV_BLOCK (0xFFFF), or past the end
+    # of the table row, are left out of the softmax instead of being read
+    # from an arbitrary page.
+    banner("decode with invalid pages in the block table")
+    import torch
+    sc = Scenario(n_layer=1, n_head=8, n_kv=2, head_dim=128, block_tokens=32,
+                  lens=[300, 1000], seed=41)
+    t = sc.tables_host.copy()
+    t[0, 2] = 0xFFFF          # tokens 64..95 of sequence 0
+    t[1, 5] = 0xFFFF          # tokens 160..191 of sequence 1
+    t[1, 7] = 0xFFFF          # tokens 224..255
+    sc.tables = torch.from_numpy(np.ascontiguousarray(t).view(np.int16)).to(device)
+    q = np.random.default_rng(5).standard_normal((2, 8 * 128)).astype(np.float32)
+    got = sc.gpu_decode(0, q)
+    for s, n in enumerate(sc.lens):
+        keep = np.array([t[s, p // 32] != 0xFFFF for p in range(n)])
+        k = oracle.fp16_to_fp32(oracle.fp32_to_fp16(sc.k_rows[0][s]))[keep]
+        v = oracle.fp16_to_fp32(oracle.fp32_to_fp16(sc.v_rows[0][s]))[keep]
+        qr = oracle.fp16_to_fp32(oracle.fp32_to_fp16(q[s]))
+        want = oracle.attention_f64(qr, k, v, 8, 2, 128, int(keep.sum()), 1 / np.sqrt(128))
+        assert_close(got[s], want, what=f"seq {s} with invalid pages")
+    # a kv_len reaching past the table row: only the covered tokens count
+    sc2 = Scenario(n_layer=1, n_head=8, n_kv=2, head_dim=128, block_tokens=32, lens=[200],
+                   seed=42)
+    short = torch.from_numpy(np.ascontiguousarray(sc2.tables_host[:, :4]).view(np.int16)).to(device)
+    sc2.tables = short  # covers 128 tokens
+    got2 = sc2.gpu_decode(0, q[:1])
+    k = oracle.fp16_to_fp32(oracle.fp32_to_fp16(sc2.k_rows[0][0]))[:128]
+    v = oracle.fp16_to_fp32(oracle.fp32_to_fp16(sc2.v_rows[0][0]))[:128]
+    qr = oracle.fp16_to_fp32(oracle.fp32_to_fp16(q[0]))
+    assert_close(got2[0], oracle.attention_f64(qr, k, v, 8, 2, 128, 128, 1 / np.sqrt(128)),
+                 what="short table")
+
+
+def test_decode_graph_replay_matches_eager(device):
+    # One layer's append + decode captured in a HIP graph and replayed with
+    # eager work and synchronisations in between: every replay must equal
+    # the eager result bit for bit.
+    banner("decode step in a HIP graph, replayed")
+    import torch
+    sc = Scenario(n_layer=1, n_head=32, n_kv=8, head_dim=128, block_tokens=32,
+                  lens=[2000, 3000], seed=43, extra_blocks=4)
+    for s in range(2):
+        assert sc.actor.allocate_slots(s, 1)[0]
+    sc.refresh_tables()
+    pos = torch.tensor(sc.lens, dtype=torch.int32, device=device)
+    kl = pos + 1
+    newk = torch.randn(2, 1, 1024, device=device)
+    newv = torch.randn(2, 1, 1024, device=device)
+    q = torch.randn(2, 32, 128, device=device)
+    out = torch.zeros_like(q)
+    ws = torch.empty(emelk.decode_workspace_bytes(sc.g, 2, 3001) // 4 + 1, device=device)
+
+    def run():
+        emelk.append(sc.g, sc.k_pool, sc.v_pool, 0, newk, newv, pos, sc.tables)
+        emelk.decode(sc.g, sc.k_pool, sc.v_pool, 0, q, out, kl, 3001, sc.tables,
+                     1 / np.sqrt(128), ws)
+
+    run()
+    torch.cuda.synchronize()
+    eager = out.clone()
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            run()
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    for i in range(4):
+        out.fill_(float("nan"))
+        scratch = torch.randn(1 << 20, device=device) * 2  # unrelated eager work
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i} differs"
+        del scratch
