@@ -21,8 +21,9 @@
 //   A second kernel merges the splits.
 //
 // q8_0 pools: identical structure; for scores the 16 int8 values of a lane
-// are turned into exact fp16 with a byte-permute + packed subtract and the
-// lane's block scale multiplies its partial score; for P.V the int8 values
+// are turned into exact fp16 (biased by a constant that the dot product's
+// start value removes) with byte permutes, and the lane's block scale
+// multiplies its partial score; for P.V the int8 values
 // go to fp32 and the token scale folds into an fp32 weight p * d_v.
 #include <hip/hip_runtime.h>
 
@@ -40,6 +41,11 @@ using namespace emelk::dev;
 
 constexpr int k_max_wpb = 8;  // waves (KV heads) per workgroup
 constexpr int k_max_split_pages = 1024;
+// Register sets of tile rows kept in flight.  Measured on MI355X at the
+// Llama-3-8B shape: 3 sets (246 VGPRs) stream no faster than 2 (214), and 4
+// spill; a read-only walk of the same 64 KiB pages tops out at 6.76 TB/s,
+// which 2 sets already reach within 5%.
+constexpr int k_decode_nb = 2;
 
 // Waves per workgroup = KV heads per workgroup: min(n_head_kv, 8) when it
 // divides n_head_kv, else 1.
@@ -66,16 +72,17 @@ struct decode_params {
   float *part_ml;   // [n_seq][n_head][max_splits][2]
 };
 
-// 16 int8 -> 8 exact half2: byte b becomes the fp16 bit pattern 0x64XX with
-// XX = b + 128 (value 1024 + b + 128), then 1152 is subtracted.
-__device__ __forceinline__ void i8x16_to_half(const uint4_t w, half2_t out[8]) {
+// 16 int8 -> 8 half2 holding b + 1152 exactly: byte b becomes the fp16 bit
+// pattern 0x64XX with XX = b + 128, whose value is 1024 + b + 128.  The
+// constant 1152 is removed from the dot product by starting it at
+// -1152 * (sum of the lane's q values), so no per-value subtract is needed.
+__device__ __forceinline__ void i8x16_to_half_biased(const uint4_t w, half2_t out[8]) {
   const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-  const half2_t bias = {static_cast<half_t>(1152.0f), static_cast<half_t>(1152.0f)};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t u = ws[i] ^ 0x80808080u;
-    out[2 * i] = as_half2(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - bias;
-    out[2 * i + 1] = as_half2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - bias;
+    out[2 * i] = as_half2(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u));
+    out[2 * i + 1] = as_half2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u));
   }
 }
 
@@ -130,6 +137,28 @@ __device__ __forceinline__ void load_row(const uint8_t *__restrict__ region_base
   }
 }
 
+// Same rows, addressed as a wave-uniform base plus a fixed per-lane 32-bit
+// offset, so the loads take the scalar-base form and need no per-lane 64-bit
+// address arithmetic.  `region` is the (page, head) region, `row0` the
+// page offset of the wave's first row (both uniform); `lane_off` and
+// `lane_sc_off` are the lane's byte offsets of its values and of its q8_0
+// block scale relative to that row.
+template <int D, bool Q8>
+__device__ __forceinline__ void load_row_uniform(const uint8_t *__restrict__ region, int32_t row0,
+                                                 uint32_t lane_off, uint32_t lane_sc_off,
+                                                 int32_t bt, row_regs<D, Q8> &r) {
+  if constexpr (!Q8) {
+    const uint8_t *u = region + static_cast<uint32_t>(row0) * (2u * D);
+    r.a = load16_stream(u + lane_off);
+    r.b = load16_stream(u + lane_off + D);
+  } else {
+    const uint8_t *u = region + static_cast<uint32_t>(row0) * static_cast<uint32_t>(D);
+    r.a = load16_stream(u + lane_off);
+    const uint8_t *s = region + static_cast<uint32_t>(bt) * D + static_cast<uint32_t>(row0) * (D / 16);
+    r.d = load2_stream(s + lane_sc_off);
+  }
+}
+
 template <int D, bool Q8>
 __device__ __forceinline__ void to_half(const row_regs<D, Q8> &r, half2_t h[8], float &scale) {
   if constexpr (!Q8) {
@@ -138,7 +167,7 @@ __device__ __forceinline__ void to_half(const row_regs<D, Q8> &r, half2_t h[8], 
     for (int j = 0; j < 8; ++j) h[j] = as_half2(w[j]);
     scale = 1.0f;
   } else {
-    i8x16_to_half(r.a, h);
+    i8x16_to_half_biased(r.a, h);
     scale = f16_bits_to_f32(static_cast<uint16_t>(r.d));
   }
 }
@@ -157,6 +186,7 @@ struct decode_state {
   float l[G];
   float acc[G][16];
   float corr[G];     // q8_0: sum of P.V weights (undoes the +128 byte bias)
+  float kbias[G];    // q8_0: -1152 * sum of the lane's 16 q values (K byte bias)
 };
 
 template <int D, bool Q8>
@@ -177,7 +207,8 @@ __device__ __forceinline__ void consume_tile(decode_state<D, G, Q8> &S, const ti
   float y0[G], y1[G];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
-    float a = 0.0f, b = 0.0f;
+    float a = Q8 ? S.kbias[h] : 0.0f;
+    float b = a;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       a = dot2(S.qh[h][j], kh0[j], a);
@@ -264,7 +295,7 @@ __device__ __forceinline__ void consume_tile(decode_state<D, G, Q8> &S, const ti
 // UNIFORM: block_tokens is a multiple of the wave's lane-group count NGW, so
 // every row of a (tile, half) lies in one page: the page id is moved to a
 // scalar register once per half-tile and each lane adds a fixed offset.
-template <int D, int G, bool Q8, bool UNIFORM, int WPB>
+template <int D, int G, bool Q8, bool UNIFORM, int WPB, int NB>
 __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
   constexpr int LPT = D / 16;         // lanes per token row
   constexpr int NGW = k_wave / LPT;   // token groups per wave
@@ -276,7 +307,9 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
   const int32_t split = blockIdx.x;
   const int32_t seq = blockIdx.z;
   const int32_t tid = threadIdx.x;
-  const int32_t wave = tid / k_wave;
+  // the wave index is uniform; readfirstlane lets the compiler keep the
+  // head's base pointers in scalar registers
+  const int32_t wave = __builtin_amdgcn_readfirstlane(tid / k_wave);
   const int32_t lane = tid % k_wave;
   const int32_t kvh = blockIdx.y * WPB + wave;
   const int32_t len = P.kv_lens[seq];
@@ -305,6 +338,11 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
   const uint8_t *v_base = P.v_pool + static_cast<uint64_t>(P.layer) * P.L.layer_bytes +
                           static_cast<uint64_t>(kvh) * P.L.region_bytes;
   const uint64_t page_bytes = P.L.page_bytes;
+  // per-lane offsets of the UNIFORM path: row `grp` of the wave's rows
+  const uint32_t lane_off =
+      static_cast<uint32_t>(grp) * (Q8 ? D : 2 * D) + static_cast<uint32_t>(lane_in_row) * 16u;
+  const uint32_t lane_sc_off =
+      static_cast<uint32_t>(grp) * (D / 16) + static_cast<uint32_t>(lane_in_row / 2) * 2u;
 
   decode_state<D, G, Q8> S;
 #pragma unroll
@@ -317,6 +355,12 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
       S.qh[h][2 * j] = pack_half2(f.x, f.y);
       S.qh[h][2 * j + 1] = pack_half2(f.z, f.w);
     }
+    float qsum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      qsum += static_cast<float>(S.qh[h][j].x) + static_cast<float>(S.qh[h][j].y);
+    }
+    S.kbias[h] = -1152.0f * qsum;
     S.m[h] = -INFINITY;
     S.l[h] = 0.0f;
     S.corr[h] = 0.0f;
@@ -336,16 +380,16 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
           hb ? __builtin_amdgcn_readfirstlane(s_pages[tb / bt - first_page]) : pa;
       const bool va = pa != 0xFFFFFFFFu;
       const bool vb = pb != 0xFFFFFFFFu && hb;
-      const int32_t offa = ta % bt + grp;
-      const int32_t offb = (hb ? tb % bt : ta % bt) + grp;
+      const int32_t rowa = ta % bt;
+      const int32_t rowb = hb ? tb % bt : rowa;
       ok0 = va && ta + grp < end;
       ok1 = vb && tb + grp < end;
       const uint64_t ra = static_cast<uint64_t>(va ? pa : 0u) * page_bytes;
       const uint64_t rb = static_cast<uint64_t>(pb != 0xFFFFFFFFu ? pb : 0u) * page_bytes;
-      load_row<D, Q8>(k_base + ra, offa, lane_in_row, bt, T.k0);
-      load_row<D, Q8>(k_base + rb, offb, lane_in_row, bt, T.k1);
-      load_row<D, Q8>(v_base + ra, offa, lane_in_row, bt, T.v0);
-      load_row<D, Q8>(v_base + rb, offb, lane_in_row, bt, T.v1);
+      load_row_uniform<D, Q8>(k_base + ra, rowa, lane_off, lane_sc_off, bt, T.k0);
+      load_row_uniform<D, Q8>(k_base + rb, rowb, lane_off, lane_sc_off, bt, T.k1);
+      load_row_uniform<D, Q8>(v_base + ra, rowa, lane_off, lane_sc_off, bt, T.v0);
+      load_row_uniform<D, Q8>(v_base + rb, rowb, lane_off, lane_sc_off, bt, T.v1);
     } else {
       const int32_t t0r = tbase + grp;
       const int32_t t1r = tbase + grp + NGW;
@@ -374,24 +418,35 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
   int32_t base = start;
   if (n_full > 0) {
     // Loads are unconditional (a load past the last full tile re-reads the
-    // split's first tile and is discarded): no branch around them, so the
-    // compiler's wait counters can keep them in flight across the consume.
+    // last full tile and is discarded): no branch around them, so the
+    // compiler's wait counters keep NB - 1 tiles in flight across each
+    // consume.  Register set j is only ever touched at unrolled position j.
     const int32_t last_full = start + (n_full - 1) * TT;
-    tile_regs<D, Q8> A, B;
+    tile_regs<D, Q8> R[NB];
     bool u0, u1;
-    load_tile(base, A, u0, u1);
-    for (int32_t i = 0; i + 1 < n_full; i += 2) {
-      load_tile(base + TT, B, u0, u1);
-      consume_tile<D, G, Q8, false>(S, A, true, true, P.c);
-      base += TT;
-      const int32_t nb = base + TT <= last_full ? base + TT : start;
-      load_tile(nb, A, u0, u1);
-      consume_tile<D, G, Q8, false>(S, B, true, true, P.c);
-      base += TT;
+#pragma unroll
+    for (int j = 0; j + 1 < NB; ++j) {
+      const int32_t t = start + j * TT;
+      load_tile(t <= last_full ? t : last_full, R[j], u0, u1);
     }
-    if (n_full & 1) {
-      consume_tile<D, G, Q8, false>(S, A, true, true, P.c);
-      base += TT;
+    const int32_t n_groups = n_full / NB;
+    for (int32_t i = 0; i < n_groups; ++i) {
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        const int32_t t = base + (NB - 1) * TT;
+        load_tile(t <= last_full ? t : last_full, R[(j + NB - 1) % NB], u0, u1);
+        consume_tile<D, G, Q8, false>(S, R[j], true, true, P.c);
+        base += TT;
+      }
+    }
+    // the remaining n_full % NB tiles are already loaded into R[0..]
+    const int32_t rem = n_full - n_groups * NB;
+#pragma unroll
+    for (int j = 0; j + 1 < NB; ++j) {
+      if (j < rem) {
+        consume_tile<D, G, Q8, false>(S, R[j], true, true, P.c);
+        base += TT;
+      }
     }
   }
   for (; base < end; base += TT) {
@@ -538,9 +593,9 @@ template <int D, int G, bool Q8, int WPB>
 void launch_decode_wpb(const decode_params &P, dim3 grid, hipStream_t st) {
   constexpr int NGW = k_wave / (D / 16);
   if (P.L.block_tokens % NGW == 0) {
-    hipLaunchKernelGGL((decode_kernel<D, G, Q8, true, WPB>), grid, dim3(WPB * k_wave), 0, st, P);
+    hipLaunchKernelGGL((decode_kernel<D, G, Q8, true, WPB, k_decode_nb>), grid, dim3(WPB * k_wave), 0, st, P);
   } else {
-    hipLaunchKernelGGL((decode_kernel<D, G, Q8, false, WPB>), grid, dim3(WPB * k_wave), 0, st,
+    hipLaunchKernelGGL((decode_kernel<D, G, Q8, false, WPB, k_decode_nb>), grid, dim3(WPB * k_wave), 0, st,
                        P);
   }
 }

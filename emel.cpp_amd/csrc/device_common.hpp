@@ -43,10 +43,13 @@ __device__ __forceinline__ float dot2(half2_t a, half2_t b, float c) {
 }
 
 // DPP cross-lane moves inside 16-lane rows (gfx9 encodings).
+// All controls used here read a valid lane for every lane, so no "old"
+// value is needed (mov_dpp), which lets the compiler fold the move into the
+// consuming v_add_f32_dpp.
 template <int ctrl>
 __device__ __forceinline__ float dpp(float v) {
-  return __builtin_bit_cast(
-      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), ctrl, 0xF, 0xF, false));
+  return __builtin_bit_cast(float,
+                            __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), ctrl, 0xF, 0xF, true));
 }
 constexpr int k_dpp_quad_xor1 = 0xB1;  // quad_perm [1,0,3,2]
 constexpr int k_dpp_quad_xor2 = 0x4E;  // quad_perm [2,3,0,1]
