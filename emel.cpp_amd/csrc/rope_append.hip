@@ -1,0 +1,317 @@
+// The step before append, fused into one launch: optional head-wise RMS
+// norm of q and k, optional RMS norm of v, RoPE of q and k, and the append
+// of k and v into the paged pool (f16 or q8_0).  Restates the part of
+// compute_layer_attention_residual between the Q/K/V projections and
+// store_attention_kv_cache (text/generator/detail.hpp:3806-3825) and the same
+// steps of the chunked-prefill row loop (detail.hpp:4335-4360).
+//
+// Every product and sum is evaluated unfused in the reference's order
+// (floating-point contraction is off for this whole file), and division and
+// square root are the correctly rounded IEEE ones (hipcc's default
+// -fhip-fp32-correctly-rounded-divide-sqrt; __fsqrt_rn would be the native,
+// 1-ulp v_sqrt_f32), so the results are bit-exact against that arithmetic.  cos/sin come from a
+// table built on the host with the reference's recurrence.
+//
+// Launch: one workgroup of 4 waves per (token, group of 4 rows), where the
+// rows of a token are its n_head q heads, n_head_kv k heads and n_head_kv v
+// heads.  A wave stages its row of head_dim floats in LDS.  This is a few KB
+// per token: latency, not bandwidth, bounds it.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <new>
+#include <vector>
+
+#include "device_common.hpp"
+#include "emelk.h"
+#include "pool_layout.hpp"
+#include "q8_device.hpp"
+
+#pragma clang fp contract(off)
+
+struct emelk_rope_table {
+  emelk_rope_params params;
+  int32_t head_dim = 0;
+  int32_t pair_count = 0;
+  int32_t x1_base = 0;
+  int32_t max_positions = 0;
+  float2 *dev = nullptr;  // [max_positions][pair_count] (cos, sin)
+};
+
+namespace emelk {
+namespace {
+
+using namespace emelk::dev;
+
+constexpr int k_rows_per_wg = 4;
+constexpr int k_max_dim = 128;
+
+struct rope_append_args {
+  pool_layout L;
+  uint8_t *k_pool;
+  uint8_t *v_pool;
+  int32_t layer;
+  const float *q_in;
+  float *q_out;
+  const float *k_rows;
+  const float *v_rows;
+  int32_t n_tokens;
+  const int32_t *positions;
+  const uint16_t *tables;
+  int32_t table_stride;
+  const float2 *rope;
+  int32_t rope_positions;
+  int32_t pair_count;
+  int32_t x0_stride;
+  int32_t x1_stride;
+  int32_t x1_base;
+  const float *q_norm;
+  const float *k_norm;
+  int32_t v_rms;
+  float eps;
+};
+
+__global__ __launch_bounds__(k_rows_per_wg *k_wave) void rope_append_kernel(rope_append_args A) {
+  __shared__ __align__(16) float s_row[k_rows_per_wg][k_max_dim];  // float4 reads (q8_0)
+  __shared__ float s_scale[k_rows_per_wg];
+
+  const pool_layout &L = A.L;
+  const int32_t D = L.head_dim;
+  const int32_t s = blockIdx.x / A.n_tokens;
+  const int32_t t = blockIdx.x % A.n_tokens;
+  const int32_t pos = A.positions[s] + t;
+  // Token validity is uniform over the workgroup, so the early exit keeps
+  // every barrier below uniform.
+  if (pos < 0) return;
+  if (A.pair_count > 0 && pos >= A.rope_positions) return;
+  const int32_t lb = pos / L.block_tokens;
+  if (lb >= A.table_stride) return;
+  const uint32_t page = A.tables[static_cast<uint64_t>(s) * A.table_stride + lb];
+  if (page >= static_cast<uint32_t>(L.max_blocks)) return;
+  const int32_t slot = pos % L.block_tokens;
+
+  const int32_t wave = threadIdx.x / k_wave;
+  const int32_t lane = threadIdx.x % k_wave;
+  const int32_t row = blockIdx.y * k_rows_per_wg + wave;
+  const int32_t n_rows = L.n_head + 2 * L.n_head_kv;
+  const bool have = row < n_rows;
+  const int32_t kind = row < L.n_head ? 0 : (row < L.n_head + L.n_head_kv ? 1 : 2);
+  const int32_t head = kind == 0 ? row : (kind == 1 ? row - L.n_head : row - L.n_head - L.n_head_kv);
+  const uint64_t tok = static_cast<uint64_t>(s) * A.n_tokens + t;
+  const float *src = nullptr;
+  if (have) {
+    if (kind == 0) {
+      src = A.q_in + (tok * L.n_head + head) * static_cast<uint64_t>(D);
+    } else {
+      src = (kind == 1 ? A.k_rows : A.v_rows) + (tok * L.n_head_kv + head) * static_cast<uint64_t>(D);
+    }
+  }
+  float *buf = s_row[wave];
+  if (have) {
+    for (int32_t d = lane; d < D; d += k_wave) buf[d] = src[d];
+  }
+  __syncthreads();
+
+  // Norm scale, computed by one lane in the reference's summation order.
+  const float *wt = kind == 0 ? A.q_norm : (kind == 1 ? A.k_norm : nullptr);
+  const bool head_norm = have && kind < 2 && wt != nullptr;
+  const bool v_norm = have && kind == 2 && A.v_rms != 0;
+  if (lane == 0 && head_norm) {
+    // apply_headwise_rms_norm (detail.hpp:1073-1082)
+    float ss = 0.0f;
+    for (int32_t d = 0; d < D; ++d) ss += buf[d] * buf[d];
+    s_scale[wave] = 1.0f / sqrtf(ss / static_cast<float>(D) + A.eps);
+  }
+  if (lane == 0 && v_norm) {
+    // apply_rms_norm_in_place (detail.hpp:1098-1106) over the token's whole v
+    const float *v = A.v_rows + tok * L.n_head_kv * static_cast<uint64_t>(D);
+    const int32_t n = L.n_head_kv * D;
+    double ss = 0.0;
+    for (int32_t i = 0; i < n; ++i) ss += static_cast<double>(v[i] * v[i]);
+    const float mean = static_cast<float>(ss / static_cast<double>(n));
+    s_scale[wave] = 1.0f / sqrtf(mean + A.eps);
+  }
+  __syncthreads();
+  if (head_norm) {
+    const float inv = s_scale[wave];
+    for (int32_t d = lane; d < D; d += k_wave) buf[d] *= inv * wt[d];
+  } else if (v_norm) {
+    const float sc = s_scale[wave];
+    for (int32_t d = lane; d < D; d += k_wave) buf[d] *= sc;
+  }
+  __syncthreads();
+
+  // apply_rope_pairing (detail.hpp:2905-2936): lane p rotates pair p.
+  if (have && kind < 2 && lane < A.pair_count) {
+    const int32_t d0 = lane * A.x0_stride;
+    const int32_t d1 = lane * A.x1_stride + A.x1_base;
+    const float2 cs = A.rope[static_cast<uint64_t>(pos) * A.pair_count + lane];
+    const float x0 = buf[d0];
+    const float x1 = buf[d1];
+    buf[d0] = x0 * cs.x - x1 * cs.y;
+    buf[d1] = x0 * cs.y + x1 * cs.x;
+  }
+  __syncthreads();
+  if (!have) return;
+
+  if (kind == 0) {
+    float *dst = A.q_out + (tok * L.n_head + head) * static_cast<uint64_t>(D);
+    for (int32_t d = lane; d < D; d += k_wave) dst[d] = buf[d];
+    return;
+  }
+  uint8_t *region = (kind == 1 ? A.k_pool : A.v_pool) +
+                    L.region_offset(A.layer, static_cast<int32_t>(page), head);
+  if (L.kv_type == EMELK_KV_F16) {
+    // store_fp16_rounded_cache (detail.hpp:3050-3055): RNE per value
+    uint32_t *dst = reinterpret_cast<uint32_t *>(region + static_cast<uint64_t>(slot) * D * 2u);
+    for (int32_t j = lane; j < D / 2; j += k_wave) dst[j] = as_u32(pack_half2(buf[2 * j], buf[2 * j + 1]));
+  } else {
+    const int32_t blocks = D / 32;
+    if (lane < blocks) {
+      int8_t qs[32];
+      uint16_t dq;
+      quantize_block32(buf + 32 * lane, qs, dq);
+      uint4_t *dst = reinterpret_cast<uint4_t *>(region + static_cast<uint64_t>(slot) * D +
+                                                 static_cast<uint64_t>(lane) * 32u);
+      dst[0] = __builtin_bit_cast(uint4_t, *reinterpret_cast<int8_t(*)[16]>(qs));
+      dst[1] = __builtin_bit_cast(uint4_t, *reinterpret_cast<int8_t(*)[16]>(qs + 16));
+      reinterpret_cast<uint16_t *>(region + L.scale_plane())[static_cast<uint64_t>(slot) * blocks +
+                                                             lane] = dq;
+    }
+  }
+}
+
+// Checks a pairing: every pair inside the head and no dim used twice.
+bool pairing_ok(const emelk_rope_params &p, int32_t head_dim, int32_t pair_count, int32_t x1_base) {
+  if (p.x0_stride < 0 || p.x1_stride < 0 || x1_base < 0) return false;
+  std::vector<char> used(static_cast<size_t>(head_dim), 0);
+  for (int32_t i = 0; i < pair_count; ++i) {
+    const int64_t d0 = static_cast<int64_t>(i) * p.x0_stride;
+    const int64_t d1 = static_cast<int64_t>(i) * p.x1_stride + x1_base;
+    if (d0 >= head_dim || d1 >= head_dim || d0 == d1) return false;
+    if (used[static_cast<size_t>(d0)] || used[static_cast<size_t>(d1)]) return false;
+    used[static_cast<size_t>(d0)] = 1;
+    used[static_cast<size_t>(d1)] = 1;
+  }
+  return true;
+}
+
+}  // namespace
+}  // namespace emelk
+
+extern "C" emel_error_type emelk_rope_table_create(const emelk_rope_params *params,
+                                                   int32_t head_dim, int32_t max_positions,
+                                                   void *stream, emelk_rope_table **table_out) {
+  if (table_out == nullptr) return EMELK_ERR_INVALID_REQUEST;
+  *table_out = nullptr;
+  if (params == nullptr || head_dim <= 0 || head_dim > emelk::k_max_dim || max_positions <= 0 ||
+      !(params->freq_base > 0.0f) || !std::isfinite(params->freq_base)) {
+    return EMELK_ERR_INVALID_REQUEST;
+  }
+  const int32_t rot_dim = params->n_rot < head_dim ? params->n_rot : head_dim;
+  // apply_rope_pairing leaves the vector unchanged when rot_dim <= 1
+  const int32_t pair_count = rot_dim > 1 ? rot_dim / 2 : 0;
+  const int64_t x1_base_wide = static_cast<int64_t>(params->x1_offset) +
+                               static_cast<int64_t>(params->x1_half_rot_offset) * pair_count;
+  if (x1_base_wide < 0 || x1_base_wide > head_dim) return EMELK_ERR_INVALID_REQUEST;
+  const int32_t x1_base = static_cast<int32_t>(x1_base_wide);
+  if (!emelk::pairing_ok(*params, head_dim, pair_count, x1_base)) return EMELK_ERR_INVALID_REQUEST;
+  const uint64_t entries = static_cast<uint64_t>(max_positions) * static_cast<uint64_t>(pair_count);
+  if (entries > (uint64_t{1} << 29)) return EMELK_ERR_INVALID_REQUEST;  // 4 GiB of (cos, sin)
+
+  auto *tb = new (std::nothrow) emelk_rope_table();
+  if (tb == nullptr) return EMELK_ERR_OUT_OF_MEMORY;
+  tb->params = *params;
+  tb->head_dim = head_dim;
+  tb->pair_count = pair_count;
+  tb->x1_base = x1_base;
+  tb->max_positions = max_positions;
+  if (entries > 0) {
+    std::vector<float2> host;
+    try {
+      host.resize(entries);
+    } catch (...) {
+      delete tb;
+      return EMELK_ERR_OUT_OF_MEMORY;
+    }
+    // the per-call recurrence of apply_rope_pairing (detail.hpp:2915-2934)
+    const float theta_scale = ::powf(params->freq_base, -2.0f / static_cast<float>(rot_dim));
+    for (int32_t p = 0; p < max_positions; ++p) {
+      float theta = static_cast<float>(p);
+      float2 *row = host.data() + static_cast<uint64_t>(p) * pair_count;
+      for (int32_t i = 0; i < pair_count; ++i) {
+        row[i] = make_float2(::cosf(theta), ::sinf(theta));
+        theta *= theta_scale;
+      }
+    }
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (hipMalloc(reinterpret_cast<void **>(&tb->dev), entries * sizeof(float2)) != hipSuccess) {
+      delete tb;
+      return EMELK_ERR_OUT_OF_MEMORY;
+    }
+    if (hipMemcpyAsync(tb->dev, host.data(), entries * sizeof(float2), hipMemcpyHostToDevice, st) !=
+            hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess) {
+      emelk_rope_table_destroy(tb);
+      return EMELK_ERR_BACKEND;
+    }
+  }
+  *table_out = tb;
+  return EMELK_ERR_NONE;
+}
+
+extern "C" void emelk_rope_table_destroy(emelk_rope_table *table) {
+  if (table == nullptr) return;
+  if (table->dev != nullptr) {
+    (void)hipDeviceSynchronize();
+    (void)hipFree(table->dev);
+  }
+  delete table;
+}
+
+extern "C" emel_error_type emelk_kv_qkv_rope_append(
+    const emelk_kv_geometry *g, void *k_pool, void *v_pool, int32_t layer, const float *q_in,
+    float *q_out, const float *k_rows, const float *v_rows, int32_t n_seq, int32_t n_tokens,
+    const int32_t *positions, const uint16_t *block_tables, int32_t table_stride,
+    const emelk_rope_table *rope, const float *q_norm, const float *k_norm, int32_t v_rms,
+    float rms_epsilon, void *stream) {
+  emelk::pool_layout L;
+  if (emelk::make_pool_layout(g, L) != EMELK_ERR_NONE || k_pool == nullptr || v_pool == nullptr ||
+      q_in == nullptr || q_out == nullptr || k_rows == nullptr || v_rows == nullptr ||
+      positions == nullptr || block_tables == nullptr || rope == nullptr || layer < 0 ||
+      layer >= L.n_layer || n_seq < 0 || n_tokens < 0 || table_stride <= 0 ||
+      rope->head_dim != L.head_dim || !std::isfinite(rms_epsilon) ||
+      static_cast<int64_t>(n_seq) * n_tokens > 0x7FFFFFFF) {
+    return EMELK_ERR_INVALID_REQUEST;
+  }
+  if (n_seq == 0 || n_tokens == 0) return EMELK_ERR_NONE;
+  emelk::rope_append_args A;
+  A.L = L;
+  A.k_pool = static_cast<uint8_t *>(k_pool);
+  A.v_pool = static_cast<uint8_t *>(v_pool);
+  A.layer = layer;
+  A.q_in = q_in;
+  A.q_out = q_out;
+  A.k_rows = k_rows;
+  A.v_rows = v_rows;
+  A.n_tokens = n_tokens;
+  A.positions = positions;
+  A.tables = block_tables;
+  A.table_stride = table_stride;
+  A.rope = rope->dev;
+  A.rope_positions = rope->max_positions;
+  A.pair_count = rope->pair_count;
+  A.x0_stride = rope->params.x0_stride;
+  A.x1_stride = rope->params.x1_stride;
+  A.x1_base = rope->x1_base;
+  A.q_norm = q_norm;
+  A.k_norm = k_norm;
+  A.v_rms = v_rms;
+  A.eps = rms_epsilon;
+  const int32_t n_rows = L.n_head + 2 * L.n_head_kv;
+  const dim3 grid(static_cast<uint32_t>(n_seq * n_tokens),
+                  static_cast<uint32_t>((n_rows + emelk::k_rows_per_wg - 1) / emelk::k_rows_per_wg));
+  hipLaunchKernelGGL(emelk::rope_append_kernel, grid, dim3(emelk::k_rows_per_wg * emelk::k_wave),
+                     0, static_cast<hipStream_t>(stream), A);
+  return hipGetLastError() == hipSuccess ? EMELK_ERR_NONE : EMELK_ERR_BACKEND;
+}

@@ -134,6 +134,17 @@ class Geometry(ctypes.Structure):
                 ("kv_type", ctypes.c_int32)]
 
 
+class RopeParams(ctypes.Structure):
+    _fields_ = [("n_rot", ctypes.c_int32), ("x0_stride", ctypes.c_int32),
+                ("x1_stride", ctypes.c_int32), ("x1_offset", ctypes.c_int32),
+                ("x1_half_rot_offset", ctypes.c_int32), ("freq_base", ctypes.c_float)]
+
+
+# rope_pairing presets (text/generator/detail.hpp:39-50)
+NORMAL_PAIRING = (2, 2, 1, 0)
+NEOX_PAIRING = (1, 1, 0, 1)
+
+
 # (name, restype, argtypes) for every symbol include/emelk.h declares.
 _P = ctypes.c_void_p
 _SIGNATURES = [
@@ -175,6 +186,13 @@ _SIGNATURES = [
     ("emelk_attn_prefill_chunk", ctypes.c_uint32,
      [ctypes.POINTER(Geometry), _P, _P, ctypes.c_int32, _P, _P, ctypes.c_int32, ctypes.c_int32,
       _P, _P, ctypes.c_int32, ctypes.c_float, _P]),
+    ("emelk_rope_table_create", ctypes.c_uint32,
+     [ctypes.POINTER(RopeParams), ctypes.c_int32, ctypes.c_int32, _P,
+      ctypes.POINTER(ctypes.c_void_p)]),
+    ("emelk_rope_table_destroy", None, [_P]),
+    ("emelk_kv_qkv_rope_append", ctypes.c_uint32,
+     [ctypes.POINTER(Geometry), _P, _P, ctypes.c_int32, _P, _P, _P, _P, ctypes.c_int32,
+      ctypes.c_int32, _P, _P, ctypes.c_int32, _P, _P, _P, ctypes.c_int32, ctypes.c_float, _P]),
     ("emelk_kv_cache_create", ctypes.c_uint32,
      [ctypes.POINTER(Geometry), _P, ctypes.POINTER(ctypes.c_void_p)]),
     ("emelk_kv_cache_destroy", None, [_P]),
@@ -406,3 +424,37 @@ def prefill_chunk(g, k_pool, v_pool, layer, q, out, q_start, block_tables, scale
                                         _ptr(q_start), _ptr(block_tables),
                                         int(block_tables.shape[1]), scale, _stream(stream)),
            "emelk_attn_prefill_chunk")
+
+
+class RopeTable:
+    """Device (cos, sin) table of emelk_rope_table_create."""
+
+    def __init__(self, n_rot, head_dim, max_positions, freq_base, pairing=NORMAL_PAIRING,
+                 stream=None):
+        self.params = RopeParams(n_rot, *pairing, freq_base)
+        h = ctypes.c_void_p(None)
+        _check(lib.emelk_rope_table_create(ctypes.byref(self.params), head_dim, max_positions,
+                                           _stream(stream), ctypes.byref(h)),
+               "emelk_rope_table_create")
+        self.handle = h
+
+    def close(self):
+        if self.handle:
+            lib.emelk_rope_table_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        self.close()
+
+
+def qkv_rope_append(g, k_pool, v_pool, layer, q_in, q_out, k_rows, v_rows, positions,
+                    block_tables, rope: RopeTable, q_norm=None, k_norm=None, v_rms=False,
+                    eps=1e-6, stream=None):
+    """q_in/q_out: float32 [n_seq, n_tokens, n_head*head_dim]; k_rows/v_rows:
+    float32 [n_seq, n_tokens, n_head_kv*head_dim]; all on the device."""
+    n_seq, n_tokens = int(k_rows.shape[0]), int(k_rows.shape[1])
+    _check(lib.emelk_kv_qkv_rope_append(
+        ctypes.byref(g), _ptr(k_pool), _ptr(v_pool), layer, _ptr(q_in), _ptr(q_out),
+        _ptr(k_rows), _ptr(v_rows), n_seq, n_tokens, _ptr(positions), _ptr(block_tables),
+        int(block_tables.shape[1]), rope.handle, _ptr(q_norm), _ptr(k_norm), int(bool(v_rms)),
+        eps, _stream(stream)), "emelk_kv_qkv_rope_append")

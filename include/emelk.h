@@ -265,6 +265,57 @@ emel_error_type emelk_attn_prefill_chunk(const emelk_kv_geometry *g, const void 
                                          const int32_t *q_start, const uint16_t *block_tables,
                                          int32_t table_stride, float scale, void *stream);
 
+/* RoPE parameters: the reference's rope_pairing (text/generator/detail.hpp:39-50;
+ * normal = {2, 2, 1, 0}, neox = {1, 1, 0, 1}) plus n_rot and the frequency base
+ * of apply_rope_pairing (detail.hpp:2905-2936).  Pair p rotates dims
+ * p*x0_stride and p*x1_stride + x1_offset + x1_half_rot_offset*(rot_dim/2),
+ * rot_dim = min(n_rot, head_dim). */
+typedef struct emelk_rope_params {
+  int32_t n_rot;
+  int32_t x0_stride;
+  int32_t x1_stride;
+  int32_t x1_offset;
+  int32_t x1_half_rot_offset;
+  float freq_base;
+} emelk_rope_params;
+
+/* Device table of (cos, sin) per (position, pair) for positions
+ * [0, max_positions), computed once on the host exactly as
+ * apply_rope_pairing does per call: theta = float(position), then
+ * theta *= powf(freq_base, -2/rot_dim) after each pair, cosf/sinf of each
+ * theta.  Pairings whose pairs overlap or leave the head are rejected.
+ * The table is hipMalloc'd and uploaded on `stream` (synchronously). */
+typedef struct emelk_rope_table emelk_rope_table;
+emel_error_type emelk_rope_table_create(const emelk_rope_params *params, int32_t head_dim,
+                                        int32_t max_positions, void *stream,
+                                        emelk_rope_table **table_out);
+void emelk_rope_table_destroy(emelk_rope_table *table);
+
+/* The step before append, fused: for every token of every sequence, the
+ * steps of compute_layer_attention_residual (text/generator/detail.hpp:3806-3825)
+ * and of the chunked-prefill row loop (detail.hpp:4335-4360) between the
+ * Q/K/V projections and store_attention_kv_cache:
+ *   q_norm/k_norm (optional, [head_dim]): apply_headwise_rms_norm
+ *     (detail.hpp:1060-1090) on every head of q / k;
+ *   v_rms != 0: apply_rms_norm_in_place (detail.hpp:1092-1111) on the whole
+ *     v vector of the token;
+ *   RoPE (apply_rope_pairing) on q and k at position positions[s] + t;
+ *   q_out (fp32, may alias q_in) receives q; k and v are appended to the
+ *   pools as emelk_kv_append does.
+ * q_in/q_out: fp32 [n_seq][n_tokens][n_head][head_dim]; k_rows/v_rows:
+ * fp32 [n_seq][n_tokens][n_head_kv][head_dim].  Tokens whose position is
+ * outside the rope table, the block table or the pool are skipped (nothing
+ * written).  Products and sums are evaluated unfused, in the reference's
+ * order, so results are bit-exact against that arithmetic. */
+emel_error_type emelk_kv_qkv_rope_append(const emelk_kv_geometry *g, void *k_pool, void *v_pool,
+                                         int32_t layer, const float *q_in, float *q_out,
+                                         const float *k_rows, const float *v_rows,
+                                         int32_t n_seq, int32_t n_tokens,
+                                         const int32_t *positions, const uint16_t *block_tables,
+                                         int32_t table_stride, const emelk_rope_table *rope,
+                                         const float *q_norm, const float *k_norm, int32_t v_rms,
+                                         float rms_epsilon, void *stream);
+
 /* Device KV owner: allocates both pools (hipMalloc) and serves as the
  * allocate_slots copy_block callback target (text/generator/context.hpp:36-50). */
 typedef struct emelk_kv_cache emelk_kv_cache;

@@ -50,6 +50,12 @@ for name, res, args in [
     ("orc_attention_f64", None,
      [_f32p, _f32p, _f32p, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
       ctypes.c_double, _f32p]),
+    ("orc_rope_pairing", None,
+     [_f32p, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+      ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_float]),
+    ("orc_headwise_rms_norm", ctypes.c_int,
+     [_f32p, _f32p, ctypes.c_int32, ctypes.c_int32, ctypes.c_float]),
+    ("orc_rms_norm_in_place", ctypes.c_int, [_f32p, ctypes.c_int64, ctypes.c_float]),
     ("orc_decode_batch_f16", ctypes.c_double,
      [_f32p, _u16p, _u16p, _u16p, ctypes.c_int32, _i32p, ctypes.c_int32, ctypes.c_int32,
       ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_float, _f32p,
@@ -163,6 +169,50 @@ def decode_batch_f16(q, key_cache, value_cache, block_tables, position_limits, b
                                     _p(limits, _i32p), n_seq, block_tokens, n_head, n_head_kv,
                                     head_dim, n_ctx, inv_scale, _p(out, _f32p), n_threads)
     return out, float(secs)
+
+
+NORMAL_PAIRING = (2, 2, 1, 0)  # rope_pairing defaults, text/generator/detail.hpp:39-46
+NEOX_PAIRING = (1, 1, 0, 1)    # neox_rope_pairing, detail.hpp:48-50
+
+
+def rope_pairing(vec, pairing, head_count, head_dim, n_rot, position, freq_base):
+    """apply_rope_pairing on a copy of vec (head_count*head_dim floats)."""
+    out = np.array(vec, dtype=np.float32, copy=True).ravel()
+    lib.orc_rope_pairing(_p(out, _f32p), *pairing, head_count, head_dim, n_rot, position,
+                         freq_base)
+    return out
+
+
+def headwise_rms_norm(vec, weights, head_count, head_dim, eps):
+    out = np.array(vec, dtype=np.float32, copy=True).ravel()
+    w = np.ascontiguousarray(weights, dtype=np.float32)
+    assert lib.orc_headwise_rms_norm(_p(out, _f32p), _p(w, _f32p), head_count, head_dim, eps)
+    return out
+
+
+def rms_norm_in_place(vec, eps):
+    out = np.array(vec, dtype=np.float32, copy=True).ravel()
+    assert lib.orc_rms_norm_in_place(_p(out, _f32p), out.size, eps)
+    return out
+
+
+def qkv_rope_rows(q, k, v, n_head, n_head_kv, head_dim, pairing, n_rot, freq_base, position,
+                  q_norm=None, k_norm=None, v_rms=False, eps=1e-6):
+    """The reference's per-token steps between the projections and the KV
+    store (compute_layer_attention_residual, detail.hpp:3806-3825): returns
+    (q, k, v) fp32 rows after the optional norms and RoPE."""
+    q = np.array(q, dtype=np.float32, copy=True).ravel()
+    k = np.array(k, dtype=np.float32, copy=True).ravel()
+    v = np.array(v, dtype=np.float32, copy=True).ravel()
+    if q_norm is not None:
+        q = headwise_rms_norm(q, q_norm, n_head, head_dim, eps)
+    if k_norm is not None:
+        k = headwise_rms_norm(k, k_norm, n_head_kv, head_dim, eps)
+    if v_rms:
+        v = rms_norm_in_place(v, eps)
+    q = rope_pairing(q, pairing, n_head, head_dim, n_rot, position, freq_base)
+    k = rope_pairing(k, pairing, n_head_kv, head_dim, n_rot, position, freq_base)
+    return q, k, v
 
 
 def load_ref():

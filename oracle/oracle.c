@@ -32,6 +32,15 @@
  *   orc_attention_f64
  *       one-token (output = v), uniform-score (output = mean of v) and
  *       two-token closed forms.
+ *   orc_rope_pairing
+ *       position 0 is the identity; every pair keeps its norm; the result
+ *       matches a float64 rotation by the float32 theta recurrence within
+ *       a few ulp; the normal and neox pairings touch exactly the dims the
+ *       reference tests expect (detail_tests.cpp:974-1030); dims past
+ *       n_rot are untouched.
+ *   orc_headwise_rms_norm / orc_rms_norm_in_place
+ *       float64 closed form within a few ulp; unit weights and a constant
+ *       vector give rms 1; rejected shapes return 0 as the reference does.
  */
 #define _GNU_SOURCE
 #include "oracle.h"
@@ -457,4 +466,54 @@ double orc_decode_batch_f16(const float *q, const uint16_t *key_cache, const uin
   free(th);
   free(jobs);
   return (double)(t1.tv_sec - t0.tv_sec) + 1e-9 * (double)(t1.tv_nsec - t0.tv_nsec);
+}
+
+/* ---- the step before append --------------------------------------------- */
+
+void orc_rope_pairing(float *vec, int32_t x0_stride, int32_t x1_stride, int32_t x1_offset,
+                      int32_t x1_half_rot_offset, int32_t head_count, int32_t head_dim,
+                      int32_t n_rot, int32_t position, float freq_base) {
+  const int32_t rot_dim = n_rot < head_dim ? n_rot : head_dim;
+  if (head_count <= 0 || head_dim <= 1 || rot_dim <= 1) return;
+  const float theta_scale = powf(freq_base, -2.0f / (float)rot_dim);
+  const int32_t pair_count = rot_dim / 2;
+  const int32_t x1_base = x1_offset + x1_half_rot_offset * pair_count;
+  for (int32_t head = 0; head < head_count; ++head) {
+    float *h = vec + (size_t)head * (size_t)head_dim;
+    float theta = (float)position;
+    for (int32_t pair = 0; pair < pair_count; ++pair) {
+      const float c = cosf(theta);
+      const float s = sinf(theta);
+      const int32_t d0 = pair * x0_stride;
+      const int32_t d1 = pair * x1_stride + x1_base;
+      const float x0 = h[d0];
+      const float x1 = h[d1];
+      h[d0] = x0 * c - x1 * s;
+      h[d1] = x0 * s + x1 * c;
+      theta *= theta_scale;
+    }
+  }
+}
+
+int orc_headwise_rms_norm(float *vec, const float *weights, int32_t head_count, int32_t head_dim,
+                          float epsilon) {
+  if (head_count <= 0 || head_dim <= 0) return 0;
+  for (int32_t head = 0; head < head_count; ++head) {
+    float *h = vec + (size_t)head * (size_t)head_dim;
+    float square_sum = 0.0f;
+    for (int32_t d = 0; d < head_dim; ++d) square_sum += h[d] * h[d];
+    const float inv_rms = 1.0f / sqrtf(square_sum / (float)head_dim + epsilon);
+    for (int32_t d = 0; d < head_dim; ++d) h[d] *= inv_rms * weights[d];
+  }
+  return 1;
+}
+
+int orc_rms_norm_in_place(float *vec, int64_t n, float epsilon) {
+  if (n <= 0) return 0;
+  double square_sum = 0.0;
+  for (int64_t i = 0; i < n; ++i) square_sum += (double)(vec[i] * vec[i]);
+  const float mean = (float)(square_sum / (double)n);
+  const float scale = 1.0f / sqrtf(mean + epsilon);
+  for (int64_t i = 0; i < n; ++i) vec[i] *= scale;
+  return 1;
 }

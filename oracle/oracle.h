@@ -42,6 +42,18 @@ float orc_round_fp16_weight(float v);
 
 int64_t orc_physical_kv_position(const uint16_t *blocks, int32_t block_tokens, int32_t position);
 
+/* apply_rope_pairing (text/generator/detail.hpp:2905-2936) on head_count
+ * consecutive heads of head_dim floats, in place. */
+void orc_rope_pairing(float *vec, int32_t x0_stride, int32_t x1_stride, int32_t x1_offset,
+                      int32_t x1_half_rot_offset, int32_t head_count, int32_t head_dim,
+                      int32_t n_rot, int32_t position, float freq_base);
+/* apply_headwise_rms_norm (detail.hpp:1060-1090), in place; returns 0 on a
+ * rejected shape (as the reference returns false). */
+int orc_headwise_rms_norm(float *vec, const float *weights, int32_t head_count, int32_t head_dim,
+                          float epsilon);
+/* apply_rms_norm_in_place (detail.hpp:1092-1111), in place. */
+int orc_rms_norm_in_place(float *vec, int64_t n, float epsilon);
+
 /* Append one token row (fp32) for one layer into a token-major paged cache. */
 void orc_store_kv_f16(uint16_t *key_cache, uint16_t *value_cache, int32_t kv_dim,
                       const uint16_t *blocks, int32_t block_tokens, int32_t position,

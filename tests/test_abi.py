@@ -58,3 +58,31 @@ def test_kernel_entry_points_validate_before_touching_the_gpu():
     bad_cb = ctypes.c_int32(0)
     assert not emelk.lib.emelk_kv_cache_copy_block(0, 1, 16, None, ctypes.byref(bad_cb))
     assert bad_cb.value == emelk.ERR_INVALID_REQUEST
+
+
+def test_rope_table_rejects_bad_pairings_before_touching_the_gpu():
+    h = ctypes.c_void_p(None)
+
+    def create(n_rot, pairing, head_dim=128, max_pos=16, base=1e4):
+        p = emelk.RopeParams(n_rot, *pairing, base)
+        return emelk.lib.emelk_rope_table_create(ctypes.byref(p), head_dim, max_pos, None,
+                                                 ctypes.byref(h))
+
+    # overlapping pairs (p, p+1): the reference would chain them, the kernel cannot
+    assert create(128, (1, 1, 1, 0)) == emelk.ERR_INVALID_REQUEST
+    # pairs leaving the head
+    assert create(128, (4, 4, 1, 0)) == emelk.ERR_INVALID_REQUEST
+    assert create(128, (1, 1, 0, 2)) == emelk.ERR_INVALID_REQUEST
+    # bad base, head or positions
+    assert create(128, emelk.NORMAL_PAIRING, base=0.0) == emelk.ERR_INVALID_REQUEST
+    assert create(128, emelk.NORMAL_PAIRING, head_dim=256) == emelk.ERR_INVALID_REQUEST
+    assert create(128, emelk.NORMAL_PAIRING, max_pos=0) == emelk.ERR_INVALID_REQUEST
+    assert not h.value
+    # rot_dim <= 1 rotates nothing: a table with no device memory is valid
+    assert create(1, emelk.NORMAL_PAIRING) == emelk.ERR_NONE and h.value
+    emelk.lib.emelk_rope_table_destroy(h)
+    # the fused append validates its arguments first
+    g = emelk.geometry(1, 4, 2, 64, 16, 4)
+    assert emelk.lib.emelk_kv_qkv_rope_append(ctypes.byref(g), None, None, 0, None, None, None,
+                                              None, 1, 1, None, None, 1, None, None, None, 0,
+                                              1e-6, None) == emelk.ERR_INVALID_REQUEST
