@@ -76,14 +76,17 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
   constexpr int DCH = D / 32;      // 32-wide dim chunks of O
   constexpr int KROW = D + 8;      // padded LDS row (halves) of K
   constexpr int VROW = k_tile + 8; // padded LDS row (halves) of V^T
-  constexpr int PARTS = NT / k_tile;         // staging threads per key row
-  constexpr int PW = D / PARTS;              // dims per staging thread
-  static_assert(PW == 8 || PW == 4, "K staging chunk is 16 or 8 bytes");
+  // staging items per 32-key tile: K in 8-half chunks, V in (4 keys x 2 dims)
+  constexpr int KITEMS = k_tile * D / 8;
+  constexpr int VITEMS = (k_tile / 4) * (D / 2);
+  constexpr int KI = (KITEMS + NT - 1) / NT;
+  constexpr int VI = (VITEMS + NT - 1) / NT;
 
   __shared__ half_t s_k[2][k_tile][KROW];
-  __shared__ half_t s_vt[2][D][VROW];
+  constexpr int VR = 2;  // V double buffer
+  __shared__ half_t s_vt[VR][D][VROW];
   __shared__ float s_row[WAVES][32];
-  __shared__ uint32_t s_ptab[k_max_seq_pages];
+  __shared__ uint16_t s_ptab[k_max_seq_pages];
 
   // Workgroup -> (query tile, head group, sequence).  Consecutive workgroup
   // ids are spread over the 8 XCDs; the mapping gives each XCD a contiguous
@@ -148,33 +151,32 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
   float l = 0.0f;
   const float rescale_raw = k_rescale / P.c;
 
-  // staging: thread -> (key, PW-dim part) of the 32-key tile
-  const int st_part = tid % PARTS;
-  const int st_key = tid / PARTS;
   const uint64_t layer_base = static_cast<uint64_t>(P.layer) * P.L.layer_bytes +
                               static_cast<uint64_t>(kvh) * P.L.region_bytes;
   const uint16_t *table = P.tables + static_cast<uint64_t>(seq) * P.table_stride;
+  // LDS copy of the page list; `clean` when every page the workgroup reads
+  // is valid (keys on an invalid page are left out of the softmax, as in
+  // decode, and staged as zeros).
+  bool clean;
   {
     const int n_pages = min((key_end + P.L.block_tokens - 1) / P.L.block_tokens,
                             k_max_seq_pages);
+    int bad = n_pages * P.L.block_tokens < key_end ? 1 : 0;
     for (int i = tid; i < n_pages; i += NT) {
       const uint32_t page = i < P.table_stride ? table[i] : 0xFFFFFFFFu;
-      s_ptab[i] = page < static_cast<uint32_t>(P.L.max_blocks) ? page : 0xFFFFFFFFu;
+      const bool ok = page < static_cast<uint32_t>(P.L.max_blocks);
+      s_ptab[i] = ok ? static_cast<uint16_t>(page) : 0xFFFFu;
+      bad |= ok ? 0 : 1;
     }
-    __syncthreads();
+    clean = __syncthreads_or(bad) == 0;
   }
-  // K staging: thread -> one PW-dim chunk (16 or 8 bytes) of one key row.
-  // V staging at D = 128: thread -> 4 consecutive keys x 2 dims (lane-fast
-  // dims keep each key row coalesced), transposed in registers so each
-  // dim's 4 keys reach LDS as one 8-byte store in the accumulator's key
-  // order.  D = 64: one key x PW dims, stored element-wise.
-  constexpr bool VT4 = (D == 128);
-  const int vt_dp = tid % (D / 2);       // dim pair
-  const int vt_kg = tid / (D / 2);       // key group (4 keys)
+  // K staging: item -> one 8-half chunk of one key row.  V staging: item ->
+  // 4 consecutive keys x 2 dims (dims fastest keeps each key row coalesced),
+  // transposed in registers so each dim's 4 keys reach LDS as one 8-byte
+  // store in the accumulator's key order.
   struct stage_t {
-    uint4_t rk16;
-    uint2 rk8, rv8;
-    uint32_t rv4[4];
+    uint4_t rk[KI];
+    uint32_t rv[VI][4];
   };
 
   // Page of a key from the LDS copy of this sequence's page list (no
@@ -185,71 +187,136 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
     const int lb = bt_shift >= 0 ? key >> bt_shift : key / bt;
     const int row = bt_shift >= 0 ? key & (bt - 1) : key % bt;
     // a sequence holds at most k_max_seq_pages pages (MAX_BLOCKS_PER_SEQUENCE)
-    const uint32_t page = (key < total && lb < k_max_seq_pages) ? s_ptab[lb] : 0xFFFFFFFFu;
-    ok = page != 0xFFFFFFFFu ? 1u : 0u;
+    const uint32_t page = (key < total && lb < k_max_seq_pages) ? s_ptab[lb] : 0xFFFFu;
+    ok = page != 0xFFFFu ? 1u : 0u;
     return layer_base + static_cast<uint64_t>(ok ? page : 0u) * P.L.page_bytes +
            static_cast<uint64_t>(row) * D * 2u;
   };
-  auto load_tile = [&](int t, stage_t &R) {
-    {
-      uint32_t ok;
-      const uint64_t off = key_offset(t * k_tile + st_key, ok) + st_part * PW * 2u;
-      if constexpr (PW == 8) {
-        R.rk16 = ok ? load16(P.k_pool + off) : uint4_t{0u, 0u, 0u, 0u};
-      } else {
-        R.rk8 = ok ? *reinterpret_cast<const uint2 *>(P.k_pool + off) : uint2{0u, 0u};
-        R.rv8 = ok ? *reinterpret_cast<const uint2 *>(P.v_pool + off) : uint2{0u, 0u};
+  // Uniform tiles (block_tokens a multiple of 32): a 32-key tile lies in one
+  // page, so its base address is wave-uniform and every thread adds fixed
+  // offsets; loads are unconditional.  Keys past the sequence end get zero V
+  // (their P is 0, and 0 * garbage could be NaN); a tile on an invalid page
+  // is all zeros, as the general path gives.
+  const bool uniform_tiles = bt_shift >= 5;
+  uint32_t kofs[KI], vofs[VI];
+#pragma unroll
+  for (int i = 0; i < KI; ++i) {
+    const int item = tid + i * NT;
+    kofs[i] = static_cast<uint32_t>((item / (D / 8)) * D * 2 + (item % (D / 8)) * 16);
+  }
+#pragma unroll
+  for (int i = 0; i < VI; ++i) {
+    const int item = tid + i * NT;
+    vofs[i] = static_cast<uint32_t>(4 * (item / (D / 2)) * D * 2 + 4 * (item % (D / 2)));
+  }
+  auto load_tile_uniform = [&](int t, stage_t &R) {
+    const int key0 = t * k_tile;
+    const int lb = key0 >> bt_shift;
+    const uint32_t page = __builtin_amdgcn_readfirstlane(
+        (key0 < total && lb < k_max_seq_pages) ? static_cast<uint32_t>(s_ptab[lb]) : 0xFFFFu);
+    const bool valid = page != 0xFFFFu;
+    const uint64_t base = layer_base + static_cast<uint64_t>(valid ? page : 0u) * P.L.page_bytes +
+                          static_cast<uint64_t>(key0 & (bt - 1)) * D * 2u;
+    const uint8_t *kb = P.k_pool + base;
+    const uint8_t *vb = P.v_pool + base;
+#pragma unroll
+    for (int i = 0; i < KI; ++i) {
+      if (KITEMS % NT == 0 || tid + i * NT < KITEMS) R.rk[i] = load16(kb + kofs[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < VI; ++i) {
+      if (VITEMS % NT == 0 || tid + i * NT < VITEMS) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          R.rv[i][j] = *reinterpret_cast<const uint32_t *>(vb + vofs[i] + j * D * 2);
+        }
       }
     }
-    if constexpr (VT4) {
-      // the 4 keys share a page whenever block_tokens is a multiple of 4
-      const int key0 = t * k_tile + 4 * vt_kg;
-      const bool same_page = (bt & 3) == 0;
-      uint32_t ok0;
-      const uint64_t off0 = key_offset(key0, ok0) + 4u * vt_dp;
+    if (!valid) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        uint32_t ok = ok0;
-        uint64_t off = off0 + static_cast<uint64_t>(j) * D * 2u;
-        if (!same_page) off = key_offset(key0 + j, ok) + 4u * vt_dp;
-        ok = ok && (key0 + j < total);
-        R.rv4[j] = ok ? *reinterpret_cast<const uint32_t *>(P.v_pool + off) : 0u;
+      for (int i = 0; i < KI; ++i) R.rk[i] = uint4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int i = 0; i < VI; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) R.rv[i][j] = 0u;
+      }
+    } else if (key0 + k_tile > total) {
+#pragma unroll
+      for (int i = 0; i < VI; ++i) {
+        const int k4 = key0 + 4 * ((tid + i * NT) / (D / 2));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) R.rv[i][j] = k4 + j < total ? R.rv[i][j] : 0u;
       }
     }
   };
-  auto store_tile = [&](int buf, const stage_t &R) {
-    if constexpr (PW == 8) {
-      *reinterpret_cast<uint4_t *>(&s_k[buf][st_key][st_part * PW]) = R.rk16;
-    } else {
-      *reinterpret_cast<uint2 *>(&s_k[buf][st_key][st_part * PW]) = R.rk8;
-    }
-    if constexpr (VT4) {
-      if (vt_kg < k_tile / 4) {
-        const int slot = key_slot(4 * vt_kg);  // 4 consecutive keys -> 4 consecutive slots
-        const uint32_t lo01 = __builtin_amdgcn_perm(R.rv4[1], R.rv4[0], 0x05040100u);
-        const uint32_t lo23 = __builtin_amdgcn_perm(R.rv4[3], R.rv4[2], 0x05040100u);
-        const uint32_t hi01 = __builtin_amdgcn_perm(R.rv4[1], R.rv4[0], 0x07060302u);
-        const uint32_t hi23 = __builtin_amdgcn_perm(R.rv4[3], R.rv4[2], 0x07060302u);
-        *reinterpret_cast<uint2 *>(&s_vt[buf][2 * vt_dp][slot]) = uint2{lo01, lo23};
-        *reinterpret_cast<uint2 *>(&s_vt[buf][2 * vt_dp + 1][slot]) = uint2{hi01, hi23};
-      }
-    } else {
-      const int slot = key_slot(st_key);
-      const uint32_t w[2] = {R.rv8.x, R.rv8.y};
+  auto load_tile_general = [&](int t, stage_t &R) {
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const int dim = st_part * PW + 2 * e;
-        s_vt[buf][dim][slot] = __builtin_bit_cast(half_t, static_cast<uint16_t>(w[e] & 0xFFFFu));
-        s_vt[buf][dim + 1][slot] = __builtin_bit_cast(half_t, static_cast<uint16_t>(w[e] >> 16));
+    for (int i = 0; i < KI; ++i) {
+      const int item = tid + i * NT;
+      if (KITEMS % NT == 0 || item < KITEMS) {
+        uint32_t ok;
+        const uint64_t off = key_offset(t * k_tile + item / (D / 8), ok) + (item % (D / 8)) * 16u;
+        R.rk[i] = ok ? load16(P.k_pool + off) : uint4_t{0u, 0u, 0u, 0u};
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < VI; ++i) {
+      const int item = tid + i * NT;
+      if (VITEMS % NT == 0 || item < VITEMS) {
+        const int dp = item % (D / 2);
+        const int key0 = t * k_tile + 4 * (item / (D / 2));
+        // the 4 keys share a page whenever block_tokens is a multiple of 4
+        const bool same_page = (bt & 3) == 0;
+        uint32_t ok0;
+        const uint64_t off0 = key_offset(key0, ok0) + 4u * dp;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          uint32_t ok = ok0;
+          uint64_t off = off0 + static_cast<uint64_t>(j) * D * 2u;
+          if (!same_page) off = key_offset(key0 + j, ok) + 4u * dp;
+          ok = ok && (key0 + j < total);
+          R.rv[i][j] = ok ? *reinterpret_cast<const uint32_t *>(P.v_pool + off) : 0u;
+        }
+      }
+    }
+  };
+  auto load_tile = [&](int t, stage_t &R) {
+    if (uniform_tiles) {
+      load_tile_uniform(t, R);
+    } else {
+      load_tile_general(t, R);
+    }
+  };
+  auto store_tile = [&](int kbuf, int vbuf, const stage_t &R) {
+#pragma unroll
+    for (int i = 0; i < KI; ++i) {
+      const int item = tid + i * NT;
+      if (KITEMS % NT == 0 || item < KITEMS) {
+        *reinterpret_cast<uint4_t *>(&s_k[kbuf][item / (D / 8)][(item % (D / 8)) * 8]) = R.rk[i];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < VI; ++i) {
+      const int item = tid + i * NT;
+      if (VITEMS % NT == 0 || item < VITEMS) {
+        const int dp = item % (D / 2);
+        const int slot = key_slot(4 * (item / (D / 2)));  // 4 consecutive keys -> 4 slots
+        const uint32_t *w = R.rv[i];
+        const uint32_t lo01 = __builtin_amdgcn_perm(w[1], w[0], 0x05040100u);
+        const uint32_t lo23 = __builtin_amdgcn_perm(w[3], w[2], 0x05040100u);
+        const uint32_t hi01 = __builtin_amdgcn_perm(w[1], w[0], 0x07060302u);
+        const uint32_t hi23 = __builtin_amdgcn_perm(w[3], w[2], 0x07060302u);
+        *reinterpret_cast<uint2 *>(&s_vt[vbuf][2 * dp][slot]) = uint2{lo01, lo23};
+        *reinterpret_cast<uint2 *>(&s_vt[vbuf][2 * dp + 1][slot]) = uint2{hi01, hi23};
       }
     }
   };
 
-  // One tile: scores, online softmax, O update, from LDS buffer t & 1.
-  auto compute = [&](int t) {
+  // One tile in three steps: scores (K ring of 2), online softmax, O update
+  // (V ring of 3).
+  auto qk = [&](int t, float16_v &s) {
     const int buf = t & 1;
     // S^T = K . Q^T
-    float16_v s;
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] = 0.0f;
 #pragma unroll
@@ -257,30 +324,46 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
       const half8_v a = *reinterpret_cast<const half8_v *>(&s_k[buf][l32][16 * kk + 8 * h]);
       s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qop[kk], s, 0, 0, 0);
     }
-
-    // Online softmax for query my_row (16 keys in-lane + the other half).
-    // Only tiles reaching past the workgroup's first query position or the
-    // sequence end need the causal mask.
-    const int tile_last = t * k_tile + k_tile - 1;
-    const bool interior = tile_last <= wg_first_pos && tile_last < total;
+  };
+  // Max / sum of v and the value 32 lanes apart, by v_permlane32_swap: with
+  // both operands v the two results are v's low and high halves, so every
+  // lane gets the same (commutative) combination.
+  auto halves = [](float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v),
+                                                    __builtin_bit_cast(uint32_t, v), false, false);
+    return float2{__builtin_bit_cast(float, static_cast<uint32_t>(r[0])),
+                  __builtin_bit_cast(float, static_cast<uint32_t>(r[1]))};
+  };
+  // Online softmax for query my_row (16 keys in-lane + the other half).
+  // INTERIOR tiles lie wholly before the workgroup's first query position
+  // and inside the sequence, on valid pages: no mask.
+  auto softmax = [&]<bool INTERIOR>(int t, float16_v &s) {
     float tmax = -INFINITY;
-    if (interior) {
+    if constexpr (INTERIOR) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[r]);
     } else {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int key = t * k_tile + 8 * (r / 4) + 4 * h + (r % 4);
-        const bool ok = key <= my_pos && key < total;
-        s[r] = ok ? s[r] : -INFINITY;
-        tmax = fmaxf(tmax, s[r]);
+        s[r] = (key <= my_pos && key < total) ? s[r] : -INFINITY;
       }
+      if (!clean) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = t * k_tile + 8 * (r / 4) + 4 * h + (r % 4);
+          const int lb = bt_shift >= 0 ? key >> bt_shift : key / bt;
+          const bool ok = lb < k_max_seq_pages && s_ptab[lb] != 0xFFFFu;
+          s[r] = ok ? s[r] : -INFINITY;
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[r]);
     }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, k_wave));
-    // Scores stay raw (q.k); p = exp2(s*c - m*c) is one FMA + exp2.  Lazy
-    // rescale: the reference max moves only when a score passes it by more
-    // than 2^8 after scaling, so P <= 256 and the O rescale is skipped on
-    // almost every tile.
+    {
+      const float2 hv = halves(tmax);
+      tmax = fmaxf(hv.x, hv.y);
+    }
     const bool need = tmax > m + rescale_raw;
     float alpha = 1.0f;
     if (need) {
@@ -289,22 +372,26 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
       m = tmax;
     }
     const float mc = m * P.c;
-    float psum = 0.0f;
-    if (interior) {  // every score finite, m finite
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        s[r] = fast_exp2(fmaf(s[r], P.c, -mc));
-        psum += s[r];
-      }
-    } else {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float pr = fast_exp2(fmaf(s[r], P.c, -mc));
+    for (int r = 0; r < 16; ++r) {
+      const float pr = fast_exp2(fmaf(s[r], P.c, -mc));
+      if constexpr (INTERIOR) {  // every score finite, m finite
+        s[r] = pr;
+      } else {
         s[r] = s[r] == -INFINITY ? 0.0f : pr;  // also covers m == -inf
-        psum += s[r];
       }
     }
-    psum += __shfl_xor(psum, 32, k_wave);
+    // pairwise sum: a depth-4 tree instead of a 16-long dependent chain
+    float ps8[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) ps8[r] = s[2 * r] + s[2 * r + 1];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) ps8[r] += ps8[r + 4];
+    float psum = (ps8[0] + ps8[2]) + (ps8[1] + ps8[3]);
+    {
+      const float2 hv = halves(psum);
+      psum = hv.x + hv.y;
+    }
     l += psum;
 
     if (__builtin_amdgcn_ballot_w64(need) != 0) {
@@ -330,6 +417,9 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
       }
     }
 
+  };
+  auto pv = [&](int t, const float16_v &s) {
+    const int buf = t % VR;
     // O += P . V
     half8_v pa[2];
 #pragma unroll
@@ -345,25 +435,37 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
         o[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[st], b, o[c], 0, 0, 0);
       }
     }
-
   };
 
   // Single register stage: tile t + 1 is loaded at the start of tile t and
-  // written to the other LDS buffer after tile t's MFMAs.  Deeper register
+  // written to the free LDS buffers after tile t's work.  Deeper register
   // rings, and a software pipeline issuing tile t+1's QK MFMAs before tile
-  // t's softmax, were both measured slower: their unrolled copies push the
-  // kernel past 256 registers per lane, the budget at 8 waves per CU.
+  // t's softmax within one wave, were both measured slower: their unrolled
+  // copies push the kernel past 256 registers per lane, the budget at 8
+  // waves per CU.
+  //
+  // Tried and measured slower on MI355X: running the two waves that share a
+  // SIMD half a tile apart (one in softmax while the other issues MFMAs,
+  // with a ring of 3 V buffers), 700 vs 758 TFLOP/s; and two 4-wave
+  // workgroups per CU instead of one 8-wave workgroup, 2.6x slower.
   stage_t R;
   load_tile(0, R);
-  store_tile(0, R);
+  store_tile(0, 0, R);
   __syncthreads();
-  for (int t = 0; t < n_tiles; ++t) {
+  float16_v s;
+  // tiles [0, n_int) need no mask
+  const int n_int = clean ? min(n_tiles, min((wg_first_pos + 1) / k_tile, total / k_tile)) : 0;
+  auto step = [&]<bool INTERIOR>(int t) {
     const bool more = t + 1 < n_tiles;
     if (more) load_tile(t + 1, R);
-    compute(t);
-    if (more) store_tile((t + 1) & 1, R);
+    qk(t, s);
+    softmax.template operator()<INTERIOR>(t, s);
+    pv(t, s);
+    if (more) store_tile((t + 1) & 1, (t + 1) % VR, R);
     __syncthreads();
-  }
+  };
+  for (int t = 0; t < n_int; ++t) step.template operator()<true>(t);
+  for (int t = n_int; t < n_tiles; ++t) step.template operator()<false>(t);
 
   // normalise by l of each row and write rows < n_q
   __builtin_amdgcn_wave_barrier();
@@ -390,11 +492,12 @@ bool launch_prefill(const prefill_params &P, int32_t n_seq, hipStream_t st) {
   const int rb = 8 / g_wg;
   const int n_qt = (P.n_q + 32 * rb - 1) / (32 * rb);
   const dim3 grid(n_qt * (P.L.n_head / g_wg) * n_seq);
+  const dim3 block(8 * k_wave);
   switch (g_wg) {
-    case 1: hipLaunchKernelGGL((prefill_kernel<D, 1, 8>), grid, dim3(512), 0, st, P); return true;
-    case 2: hipLaunchKernelGGL((prefill_kernel<D, 2, 4>), grid, dim3(512), 0, st, P); return true;
-    case 4: hipLaunchKernelGGL((prefill_kernel<D, 4, 2>), grid, dim3(512), 0, st, P); return true;
-    case 8: hipLaunchKernelGGL((prefill_kernel<D, 8, 1>), grid, dim3(512), 0, st, P); return true;
+    case 1: hipLaunchKernelGGL((prefill_kernel<D, 1, 8>), grid, block, 0, st, P); return true;
+    case 2: hipLaunchKernelGGL((prefill_kernel<D, 2, 4>), grid, block, 0, st, P); return true;
+    case 4: hipLaunchKernelGGL((prefill_kernel<D, 4, 2>), grid, block, 0, st, P); return true;
+    case 8: hipLaunchKernelGGL((prefill_kernel<D, 8, 1>), grid, block, 0, st, P); return true;
     default: return false;
   }
 }

@@ -12,7 +12,7 @@ import oracle
 class Scenario:
     def __init__(self, *, n_layer, n_head, n_kv, head_dim, block_tokens, lens, kv_type=emelk.KV_F16,
                  seed=0, identity=False, outlier_frac=0.0, extra_blocks=3, device="cuda:0",
-                 fill=True):
+                 fill=True, pool_byte=0):
         import torch
         self.torch = torch
         self.n_layer, self.n_head, self.n_kv, self.D = n_layer, n_head, n_kv, head_dim
@@ -39,8 +39,9 @@ class Scenario:
         self.g = emelk.geometry(n_layer, n_head, n_kv, head_dim, block_tokens, self.max_blocks,
                                 kv_type)
         self.pool_bytes = emelk.pool_bytes(self.g)
-        self.k_pool = torch.zeros(self.pool_bytes, dtype=torch.uint8, device=device)
-        self.v_pool = torch.zeros(self.pool_bytes, dtype=torch.uint8, device=device)
+        # pool_byte 0xFF makes every never-written f16 slot a NaN
+        self.k_pool = torch.full((self.pool_bytes,), pool_byte, dtype=torch.uint8, device=device)
+        self.v_pool = torch.full((self.pool_bytes,), pool_byte, dtype=torch.uint8, device=device)
         self.refresh_tables()
         # logical fp32 rows [layer][seq] -> [len, kv_dim]
         self.k_rows, self.v_rows = [], []

@@ -341,6 +341,43 @@ def test_prefill_chunk_edges(device):
     _prefill_case(device, 16, 2, 128, 32, [64], 33, seed=34)  # G=8
 
 
+def test_prefill_masks_invalid_pages_and_never_reads_unwritten_slots(device):
+    # Pools start as 0xFF bytes (f16 NaN), so any slot past a sequence's end
+    # that reached P.V would poison the output.  Keys on invalid pages are
+    # left out of the softmax, as decode does.  bt=32 takes the uniform-page
+    # staging path, bt=16 the general one.
+    import torch
+    for bt in (32, 16):
+        banner(f"prefill on a NaN-filled pool with invalid pages, bt={bt}")
+        n_q, q_starts = 40, [100, 37]
+        lens = [q + n_q for q in q_starts]
+        sc = Scenario(n_layer=1, n_head=8, n_kv=2, head_dim=128, block_tokens=bt, lens=lens,
+                      seed=44, pool_byte=0xFF, extra_blocks=6)
+        t = sc.tables_host.copy()
+        t[0, 1] = 0xFFFF  # keys bt..2bt-1 of sequence 0
+        sc.tables = torch.from_numpy(np.ascontiguousarray(t).view(np.int16)).to(device)
+        rng = np.random.default_rng(45)
+        q = rng.standard_normal((2, n_q, 8, 128)).astype(np.float32)
+        qd = torch.from_numpy(q).to(device)
+        out = torch.full_like(qd, float("nan"))
+        emelk.prefill_chunk(sc.g, sc.k_pool, sc.v_pool, 0, qd, out,
+                            torch.tensor(q_starts, dtype=torch.int32, device=device), sc.tables,
+                            1 / np.sqrt(128))
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        assert np.isfinite(got).all()
+        for s_ in range(2):
+            kf = oracle.fp16_to_fp32(oracle.fp32_to_fp16(sc.k_rows[0][s_]))
+            vf = oracle.fp16_to_fp32(oracle.fp32_to_fp16(sc.v_rows[0][s_]))
+            for r in range(n_q):
+                limit = q_starts[s_] + r + 1
+                keep = np.array([t[s_, p // bt] != 0xFFFF for p in range(limit)])
+                qr = oracle.fp16_to_fp32(oracle.fp32_to_fp16(q[s_, r].ravel()))
+                want = oracle.attention_f64(qr, kf[:limit][keep], vf[:limit][keep], 8, 2, 128,
+                                            int(keep.sum()), 1 / np.sqrt(128))
+                assert_close(got[s_, r].ravel(), want, what=f"bt {bt} seq {s_} row {r}")
+
+
 def test_decode_masks_invalid_pages_and_short_tables(device):
     # Tokens on pages marked EMELK_INVALID_KV_BLOCK (0xFFFF), or past the end
     # of the table row, are left out of the softmax instead of being read
