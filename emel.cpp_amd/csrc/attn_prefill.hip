@@ -442,7 +442,9 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
   // rings, and a software pipeline issuing tile t+1's QK MFMAs before tile
   // t's softmax within one wave, were both measured slower: their unrolled
   // copies push the kernel past 256 registers per lane, the budget at 8
-  // waves per CU.
+  // waves per CU (the pipeline, with K staged two tiles ahead, a ring of 3
+  // V buffers and sched_group_barrier interleaving, still spilled 18
+  // registers and ran at 512 vs 809 TFLOP/s).
   //
   // Tried and measured slower on MI355X: running the two waves that share a
   // SIMD half a tile apart (one in softmax while the other issues MFMAs,
