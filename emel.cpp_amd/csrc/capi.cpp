@@ -103,6 +103,13 @@ int32_t emelk_kv_block_refs(emelk_kv_actor *a, int32_t block_id) {
   return a == nullptr ? -1 : a->impl.refs(block_id);
 }
 
+int32_t emelk_kv_sequence_length(emelk_kv_actor *a, int32_t seq_id) {
+  if (a == nullptr) return -1;
+  const auto &st = a->impl.raw();
+  if (seq_id < 0 || seq_id >= st.max_sequences || !st.active[static_cast<size_t>(seq_id)]) return -1;
+  return st.length[static_cast<size_t>(seq_id)];
+}
+
 int32_t emelk_kv_free_count(emelk_kv_actor *a) { return a == nullptr ? -1 : a->impl.free_count(); }
 
 const char *emelk_build_info(void) { return "emelk gfx950 kv-cache hot path"; }

@@ -269,6 +269,10 @@ extern "C" void emelk_rope_table_destroy(emelk_rope_table *table) {
   delete table;
 }
 
+extern "C" int32_t emelk_rope_table_positions(const emelk_rope_table *table) {
+  return table == nullptr ? 0 : table->max_positions;
+}
+
 extern "C" emel_error_type emelk_kv_qkv_rope_append(
     const emelk_kv_geometry *g, void *k_pool, void *v_pool, int32_t layer, const float *q_in,
     float *q_out, const float *k_rows, const float *v_rows, int32_t n_seq, int32_t n_tokens,

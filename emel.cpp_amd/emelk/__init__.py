@@ -193,6 +193,17 @@ _SIGNATURES = [
     ("emelk_kv_qkv_rope_append", ctypes.c_uint32,
      [ctypes.POINTER(Geometry), _P, _P, ctypes.c_int32, _P, _P, _P, _P, ctypes.c_int32,
       ctypes.c_int32, _P, _P, ctypes.c_int32, _P, _P, _P, ctypes.c_int32, ctypes.c_float, _P]),
+    ("emelk_rope_table_positions", ctypes.c_int32, [_P]),
+    ("emelk_kv_sequence_length", ctypes.c_int32, [_P, ctypes.c_int32]),
+    ("emelk_batch_decoder_create", ctypes.c_uint32,
+     [ctypes.POINTER(Geometry), _P, _P, _P, ctypes.c_int32, ctypes.c_int32, _P,
+      ctypes.POINTER(ctypes.c_void_p)]),
+    ("emelk_batch_decoder_destroy", None, [_P]),
+    ("emelk_batch_decoder_begin_step", ctypes.c_uint32,
+     [_P, c_i32p, ctypes.c_int32, ctypes.c_int32, c_i32p]),
+    ("emelk_batch_decoder_layer", ctypes.c_uint32,
+     [_P, ctypes.c_int32, _P, _P, _P, _P, _P, _P, ctypes.c_int32, ctypes.c_float, ctypes.c_float,
+      _P]),
     ("emelk_kv_cache_create", ctypes.c_uint32,
      [ctypes.POINTER(Geometry), _P, ctypes.POINTER(ctypes.c_void_p)]),
     ("emelk_kv_cache_destroy", None, [_P]),
@@ -458,3 +469,74 @@ def qkv_rope_append(g, k_pool, v_pool, layer, q_in, q_out, k_rows, v_rows, posit
         _ptr(k_rows), _ptr(v_rows), n_seq, n_tokens, _ptr(positions), _ptr(block_tables),
         int(block_tables.shape[1]), rope.handle, _ptr(q_norm), _ptr(k_norm), int(bool(v_rms)),
         eps, _stream(stream)), "emelk_kv_qkv_rope_append")
+
+
+class KvCache:
+    """Device pools owned by the library (emelk_kv_cache_create)."""
+
+    def __init__(self, g, stream=None):
+        self.g = g
+        h = ctypes.c_void_p(None)
+        _check(lib.emelk_kv_cache_create(ctypes.byref(g), _stream(stream), ctypes.byref(h)),
+               "emelk_kv_cache_create")
+        self.handle = h
+
+    def k_pool_ptr(self):
+        return lib.emelk_kv_cache_k_pool(self.handle)
+
+    def v_pool_ptr(self):
+        return lib.emelk_kv_cache_v_pool(self.handle)
+
+    def close(self):
+        if self.handle:
+            lib.emelk_kv_cache_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        self.close()
+
+
+class BatchDecoder:
+    """emelk_batch_decoder: multi-sequence steps over an actor, a cache and a
+    rope table (which must outlive it)."""
+
+    def __init__(self, g, actor: "KvActor", cache: KvCache, rope: RopeTable, max_batch,
+                 max_kv_len, stream=None):
+        self._keep = (actor, cache, rope)
+        h = ctypes.c_void_p(None)
+        _check(lib.emelk_batch_decoder_create(ctypes.byref(g), actor.handle, cache.handle,
+                                              rope.handle, max_batch, max_kv_len, _stream(stream),
+                                              ctypes.byref(h)), "emelk_batch_decoder_create")
+        self.handle = h
+
+    def begin_step(self, seq_ids, n_tokens):
+        ids = (ctypes.c_int32 * len(seq_ids))(*seq_ids)
+        pos = (ctypes.c_int32 * len(seq_ids))()
+        _check(lib.emelk_batch_decoder_begin_step(self.handle, ids, len(seq_ids), n_tokens, pos),
+               "emelk_batch_decoder_begin_step")
+        return list(pos)
+
+    def layer(self, layer, q_in, q_roped, k_rows, v_rows, out, scale, q_norm=None, k_norm=None,
+              v_rms=False, eps=1e-6):
+        _check(lib.emelk_batch_decoder_layer(self.handle, layer, _ptr(q_in), _ptr(q_roped),
+                                             _ptr(k_rows), _ptr(v_rows), _ptr(q_norm),
+                                             _ptr(k_norm), int(bool(v_rms)), eps, scale,
+                                             _ptr(out)), "emelk_batch_decoder_layer")
+
+    def close(self):
+        if self.handle:
+            lib.emelk_batch_decoder_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        self.close()
+
+
+class DevPtr:
+    """A raw device address where the helpers above expect a tensor."""
+
+    def __init__(self, address):
+        self.address = int(address)
+
+    def data_ptr(self):
+        return self.address

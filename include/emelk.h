@@ -185,6 +185,10 @@ emel_error_type emelk_kv_set_free_order(emelk_kv_actor *actor, const uint16_t *o
 /* Refcount of a physical block (kv/detail.hpp:46-97 block_pool). */
 int32_t emelk_kv_block_refs(emelk_kv_actor *actor, int32_t block_id);
 int32_t emelk_kv_free_count(emelk_kv_actor *actor);
+/* Token count of an active sequence (snapshot::sequence_length_values,
+ * view.hpp:59-117, without rebuilding the snapshot); -1 if inactive or
+ * out of range. */
+int32_t emelk_kv_sequence_length(emelk_kv_actor *actor, int32_t seq_id);
 
 /* ------------------------------------------------------------------------ */
 /* Device page pool and kernels (gfx950).                                   */
@@ -290,6 +294,8 @@ emel_error_type emelk_rope_table_create(const emelk_rope_params *params, int32_t
                                         int32_t max_positions, void *stream,
                                         emelk_rope_table **table_out);
 void emelk_rope_table_destroy(emelk_rope_table *table);
+/* Positions covered by the table (0 for NULL). */
+int32_t emelk_rope_table_positions(const emelk_rope_table *table);
 
 /* The step before append, fused: for every token of every sequence, the
  * steps of compute_layer_attention_residual (text/generator/detail.hpp:3806-3825)
@@ -328,6 +334,42 @@ void *emelk_kv_cache_v_pool(emelk_kv_cache *cache);
  * one page (all layers, K and V) on the cache's stream. */
 bool emelk_kv_cache_copy_block(int32_t src_block, int32_t dst_block, int32_t block_tokens,
                                void *user_data, int32_t *error_out);
+
+/* Multi-sequence step executor: the reference generator's per-token flow
+ * (allocate_slots with copy_kv_cache_block, text/generator/actions.hpp:460-474;
+ * capture_view, actions.hpp:270-281; per-layer compute on the sequence's
+ * block table, detail.hpp:1010-1014 and 3745-3840) for a batch of sequences
+ * instead of the single k_sequence_id = 0 (text/generator/context.hpp:33).
+ * It uses the actor, the device cache and the rope table it is given (all
+ * must outlive it) and allocates its own block-table, position and
+ * workspace buffers for up to max_batch sequences of up to max_kv_len
+ * tokens.  `stream` must be the stream the cache was created with, so page
+ * copies and kernels stay ordered. */
+typedef struct emelk_batch_decoder emelk_batch_decoder;
+emel_error_type emelk_batch_decoder_create(const emelk_kv_geometry *g, emelk_kv_actor *actor,
+                                           emelk_kv_cache *cache, const emelk_rope_table *rope,
+                                           int32_t max_batch, int32_t max_kv_len, void *stream,
+                                           emelk_batch_decoder **decoder_out);
+void emelk_batch_decoder_destroy(emelk_batch_decoder *decoder);
+/* Extends each listed sequence by n_tokens (allocate_slots; a shared tail
+ * page is split on the device through emelk_kv_cache_copy_block).  All or
+ * nothing: if one sequence is refused, the ones already extended are rolled
+ * back and its error is returned.  Uploads the block tables and positions on
+ * the stream; positions_out (host, optional) receives each sequence's first
+ * new position. */
+emel_error_type emelk_batch_decoder_begin_step(emelk_batch_decoder *decoder,
+                                               const int32_t *seq_ids, int32_t n_seq,
+                                               int32_t n_tokens, int32_t *positions_out);
+/* One layer of the open step: emelk_kv_qkv_rope_append, then attention over
+ * every sequence's history including the new tokens (emelk_attn_decode when
+ * n_tokens == 1, emelk_attn_prefill_chunk otherwise).  q_in/q_roped/out:
+ * [n_seq][n_tokens][n_head][head_dim] fp32 (q_roped may alias q_in);
+ * k_rows/v_rows: [n_seq][n_tokens][n_head_kv][head_dim] fp32. */
+emel_error_type emelk_batch_decoder_layer(emelk_batch_decoder *decoder, int32_t layer,
+                                          const float *q_in, float *q_roped, const float *k_rows,
+                                          const float *v_rows, const float *q_norm,
+                                          const float *k_norm, int32_t v_rms, float rms_epsilon,
+                                          float scale, float *out);
 
 /* Library version and the device the kernels were built for. */
 const char *emelk_build_info(void);

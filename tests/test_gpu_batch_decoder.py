@@ -1,0 +1,131 @@
+"""GPU test of the multi-sequence step executor (emelk_batch_decoder) against
+the reference's per-token flow restated by the oracle: norm + RoPE of the
+projection rows at each token's position, the store, and attention over the
+sequence's whole history (compute_layer_attention_residual,
+text/generator/detail.hpp:3745-3840), for several sequences at once,
+including a branch whose shared tail page is split on the device."""
+import numpy as np
+import pytest
+
+import emelk
+import oracle
+from kvsetup import assert_close
+
+pytestmark = pytest.mark.gpu
+
+H, HKV, D, BT, L = 8, 2, 128, 16, 2
+BASE = 1e4
+SCALE = 1.0 / np.sqrt(D)
+
+
+def banner(msg):
+    print(f"\n[gpu-case] {msg}", flush=True)
+
+
+def f16r(x):
+    return oracle.fp16_to_fp32(oracle.fp32_to_fp16(np.asarray(x, np.float32)))
+
+
+class Model:
+    """Oracle side: per sequence and layer, the stored (roped) K and V rows."""
+
+    def __init__(self):
+        self.k = {}
+        self.v = {}
+
+    def ensure(self, seq):
+        self.k.setdefault(seq, [[] for _ in range(L)])
+        self.v.setdefault(seq, [[] for _ in range(L)])
+
+    def branch(self, parent, child):
+        self.k[child] = [list(x) for x in self.k[parent]]
+        self.v[child] = [list(x) for x in self.v[parent]]
+
+    def token(self, seq, layer, q, k, v, pos, qn, kn):
+        qo, ko, vo = oracle.qkv_rope_rows(q, k, v, H, HKV, D, emelk.NEOX_PAIRING, D, BASE, pos,
+                                          q_norm=qn, k_norm=kn, eps=1e-6)
+        assert len(self.k[seq][layer]) == pos
+        self.k[seq][layer].append(ko)
+        self.v[seq][layer].append(vo)
+        kk = f16r(np.stack(self.k[seq][layer]))
+        vv = f16r(np.stack(self.v[seq][layer]))
+        return oracle.attention_f64(f16r(qo), kk, vv, H, HKV, D, pos + 1, SCALE)
+
+
+def test_batch_decoder_prefill_decode_and_branch(device):
+    import torch
+    banner("batch decoder: prefill, decode, branch with device tail split")
+    rng = np.random.default_rng(7)
+    g = emelk.geometry(L, H, HKV, D, BT, 96, emelk.KV_F16)
+    actor = emelk.KvActor()
+    assert actor.reserve(8, 96, BT)[0]
+    actor.set_free_order(rng.permutation(96).astype(np.uint16))
+    for s in range(3):
+        assert actor.allocate_sequence(s)[0]
+    cache = emelk.KvCache(g)
+    rope = emelk.RopeTable(D, D, 512, BASE, emelk.NEOX_PAIRING)
+    dec = emelk.BatchDecoder(g, actor, cache, rope, max_batch=4, max_kv_len=300)
+    qn = rng.standard_normal(D).astype(np.float32)
+    kn = rng.standard_normal(D).astype(np.float32)
+    qn_d = torch.from_numpy(qn).to(device)
+    kn_d = torch.from_numpy(kn).to(device)
+    model = Model()
+    for s in range(3):
+        model.ensure(s)
+
+    def step(ids, n_tokens, what):
+        pos = dec.begin_step(ids, n_tokens)
+        for i, s in enumerate(ids):
+            assert pos[i] == len(model.k[s][0]), f"{what}: position of seq {s}"
+        n = len(ids)
+        for layer in range(L):
+            q = rng.standard_normal((n, n_tokens, H * D)).astype(np.float32)
+            k = rng.standard_normal((n, n_tokens, HKV * D)).astype(np.float32)
+            v = rng.standard_normal((n, n_tokens, HKV * D)).astype(np.float32)
+            qd = torch.from_numpy(q).to(device)
+            out = torch.full((n, n_tokens, H * D), float("nan"), device=device)
+            dec.layer(layer, qd, qd, torch.from_numpy(k).to(device),
+                      torch.from_numpy(v).to(device), out, SCALE, q_norm=qn_d, k_norm=kn_d)
+            torch.cuda.synchronize()
+            got = out.cpu().numpy()
+            for i, s in enumerate(ids):
+                for t in range(n_tokens):
+                    want = model.token(s, layer, q[i, t], k[i, t], v[i, t], pos[i] + t, qn, kn)
+                    assert_close(got[i, t], want,
+                                 what=f"{what} layer {layer} seq {s} token {pos[i] + t}")
+
+    step([0, 1, 2], 20, "prefill")
+    step([0, 1, 2], 1, "decode 1")
+    step([2, 0, 1], 1, "decode 2")           # any order of sequences
+    # branch mid-page: seq 1 has 22 tokens, its second page is shared and
+    # partly filled, so the first append of either branch splits it on the device
+    assert actor.branch_sequence(1, 3)[0]
+    model.branch(1, 3)
+    model.ensure(3)
+    step([1, 3], 1, "after branch 1")
+    step([3, 1], 1, "after branch 2")
+    step([0, 2], 5, "prefill chunk on the others")
+    step([0, 1, 2, 3], 1, "all four")
+    dec.close()
+
+
+def test_batch_decoder_step_is_all_or_nothing(device):
+    banner("batch decoder: a refused sequence rolls the step back")
+    g = emelk.geometry(1, H, HKV, D, BT, 6, emelk.KV_F16)
+    actor = emelk.KvActor()
+    assert actor.reserve(4, 6, BT)[0]
+    for s in range(2):
+        assert actor.allocate_sequence(s)[0]
+    cache = emelk.KvCache(g)
+    rope = emelk.RopeTable(D, D, 256, BASE)
+    dec = emelk.BatchDecoder(g, actor, cache, rope, max_batch=2, max_kv_len=200)
+    dec.begin_step([0, 1], 40)               # 3 pages each: the pool of 6 is full
+    dec.begin_step([1], 8)                   # seq 1: 48 tokens, its last page full
+    free_before = emelk.lib.emelk_kv_free_count(actor.handle)
+    assert free_before == 0
+    with pytest.raises(RuntimeError):
+        dec.begin_step([0, 1], 4)            # seq 0 fits in its tail page, seq 1 does not
+    assert emelk.lib.emelk_kv_sequence_length(actor.handle, 0) == 40
+    assert emelk.lib.emelk_kv_sequence_length(actor.handle, 1) == 48
+    assert emelk.lib.emelk_kv_free_count(actor.handle) == free_before
+    dec.close()
