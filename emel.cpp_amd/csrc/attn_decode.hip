@@ -312,46 +312,56 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
   const int32_t wave = __builtin_amdgcn_readfirstlane(tid / k_wave);
   const int32_t lane = tid % k_wave;
   const int32_t kvh = blockIdx.y * WPB + wave;
+  // Start-up in one round trip: the length, q and the split's page-table
+  // entries are all requested before any of them is used (the page count
+  // of a split is bounded by tokens_per_split, so the entries are read
+  // before the length is known).
   const int32_t len = P.kv_lens[seq];
   const int32_t start = split * P.tokens_per_split;
-  if (start >= len) return;  // the combine kernel never reads this split
-  const int32_t end = min(len, start + P.tokens_per_split);
   const int32_t bt = P.L.block_tokens;
   const int32_t first_page = start / bt;
-  const int32_t n_pages = (end - 1) / bt - first_page + 1;
-
-  const uint16_t *table = P.tables + static_cast<uint64_t>(seq) * P.table_stride;
-  int bad = 0;
-  for (int32_t i = tid; i < n_pages; i += NT) {
-    const int32_t lb = first_page + i;
-    const uint32_t page = lb < P.table_stride ? table[lb] : 0xFFFFFFFFu;
-    const bool ok = page < static_cast<uint32_t>(P.L.max_blocks);
-    s_pages[i] = ok ? page : 0xFFFFFFFFu;
-    bad |= ok ? 0 : 1;
-  }
-  const bool clean = __syncthreads_or(bad) == 0;
-
   const int32_t lane_in_row = lane % LPT;
   const int32_t grp = lane / LPT;
-  const uint8_t *k_base = P.k_pool + static_cast<uint64_t>(P.layer) * P.L.layer_bytes +
-                          static_cast<uint64_t>(kvh) * P.L.region_bytes;
-  const uint8_t *v_base = P.v_pool + static_cast<uint64_t>(P.layer) * P.L.layer_bytes +
-                          static_cast<uint64_t>(kvh) * P.L.region_bytes;
-  const uint64_t page_bytes = P.L.page_bytes;
-  // per-lane offsets of the UNIFORM path: row `grp` of the wave's rows
-  const uint32_t lane_off =
-      static_cast<uint32_t>(grp) * (Q8 ? D : 2 * D) + static_cast<uint32_t>(lane_in_row) * 16u;
-  const uint32_t lane_sc_off =
-      static_cast<uint32_t>(grp) * (D / 16) + static_cast<uint32_t>(lane_in_row / 2) * 2u;
-
-  decode_state<D, G, Q8> S;
+  float4_t qraw[G][4];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
     const float *qp = P.q + (static_cast<uint64_t>(seq) * P.L.n_head + kvh * G + h) * D;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const float4_t f =
-          *reinterpret_cast<const float4_t *>(qp + lane_dim<D, Q8>(lane_in_row, 4 * j));
+      qraw[h][j] = *reinterpret_cast<const float4_t *>(qp + lane_dim<D, Q8>(lane_in_row, 4 * j));
+    }
+  }
+  constexpr int PPT = (k_max_split_pages + NT - 1) / NT;  // page entries per thread
+  const int32_t max_pages = min(k_max_split_pages, P.tokens_per_split / bt + 2);
+  const uint16_t *table = P.tables + static_cast<uint64_t>(seq) * P.table_stride;
+  uint32_t pg[PPT];
+#pragma unroll
+  for (int k = 0; k < PPT; ++k) {
+    const int32_t i = tid + k * NT;
+    const int32_t lb = first_page + i;
+    pg[k] = (i < max_pages && lb < P.table_stride) ? table[lb] : 0xFFFFFFFFu;
+  }
+  if (start >= len) return;  // uniform; the combine kernel never reads this split
+  const int32_t end = min(len, start + P.tokens_per_split);
+  const int32_t n_pages = (end - 1) / bt - first_page + 1;  // <= max_pages
+
+  int bad = 0;
+#pragma unroll
+  for (int k = 0; k < PPT; ++k) {
+    const int32_t i = tid + k * NT;
+    if (i < n_pages) {
+      const bool ok = pg[k] < static_cast<uint32_t>(P.L.max_blocks);
+      s_pages[i] = ok ? pg[k] : 0xFFFFFFFFu;
+      bad |= ok ? 0 : 1;
+    }
+  }
+  const bool clean = __syncthreads_or(bad) == 0;
+  decode_state<D, G, Q8> S;
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float4_t f = qraw[h][j];
       S.qh[h][2 * j] = pack_half2(f.x, f.y);
       S.qh[h][2 * j + 1] = pack_half2(f.z, f.w);
     }
@@ -367,6 +377,17 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) S.acc[h][i] = 0.0f;
   }
+
+  const uint8_t *k_base = P.k_pool + static_cast<uint64_t>(P.layer) * P.L.layer_bytes +
+                          static_cast<uint64_t>(kvh) * P.L.region_bytes;
+  const uint8_t *v_base = P.v_pool + static_cast<uint64_t>(P.layer) * P.L.layer_bytes +
+                          static_cast<uint64_t>(kvh) * P.L.region_bytes;
+  const uint64_t page_bytes = P.L.page_bytes;
+  // per-lane offsets of the UNIFORM path: row `grp` of the wave's rows
+  const uint32_t lane_off =
+      static_cast<uint32_t>(grp) * (Q8 ? D : 2 * D) + static_cast<uint32_t>(lane_in_row) * 16u;
+  const uint32_t lane_sc_off =
+      static_cast<uint32_t>(grp) * (D / 16) + static_cast<uint32_t>(lane_in_row / 2) * 2u;
 
   // Loads the tile at `tbase` (rows past `end` and rows on invalid pages
   // read a valid clamped address and are reported in ok0/ok1).
@@ -523,13 +544,26 @@ __global__ __launch_bounds__(D) void combine_kernel(const float *__restrict__ pa
   float mx = -INFINITY;
   for (int32_t s = 0; s < n; ++s) mx = fmaxf(mx, ml[2 * s]);
   const float ms = mx == -INFINITY ? 0.0f : mx;
-  float lsum = 0.0f, asum = 0.0f;
-  for (int32_t s = 0; s < n; ++s) {
-    const float f = fast_exp2(ml[2 * s] - ms);
-    lsum += ml[2 * s + 1] * f;
-    asum += pa[static_cast<uint64_t>(s) * D + d] * f;
+  // unrolled by 4 with independent sums so the partial loads overlap
+  float lsum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  float asum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  int32_t s = 0;
+  for (; s + 4 <= n; s += 4) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float f = fast_exp2(ml[2 * (s + u)] - ms);
+      lsum[u] += ml[2 * (s + u) + 1] * f;
+      asum[u] += pa[static_cast<uint64_t>(s + u) * D + d] * f;
+    }
   }
-  out[static_cast<uint64_t>(row) * D + d] = lsum > 0.0f ? asum / lsum : 0.0f;
+  for (; s < n; ++s) {
+    const float f = fast_exp2(ml[2 * s] - ms);
+    lsum[0] += ml[2 * s + 1] * f;
+    asum[0] += pa[static_cast<uint64_t>(s) * D + d] * f;
+  }
+  const float l = (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
+  const float a = (asum[0] + asum[1]) + (asum[2] + asum[3]);
+  out[static_cast<uint64_t>(row) * D + d] = l > 0.0f ? a / l : 0.0f;
 }
 
 struct decode_plan {
