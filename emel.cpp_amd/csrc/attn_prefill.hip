@@ -500,7 +500,11 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
   // copies push the kernel past 256 registers per lane, the budget at 8
   // waves per CU (the pipeline, with K staged two tiles ahead, a ring of 3
   // V buffers and sched_group_barrier interleaving, still spilled 18
-  // registers and ran at 512 vs 809 TFLOP/s).
+  // registers and ran at 512 vs 809 TFLOP/s).  Staging K by direct
+  // global->LDS loads (XOR-swizzled rows, issued after the tile's QK reads
+  // so no LDS read waits on them) was correct but slower: 744 TFLOP/s at
+  // 32-key tiles; at 64-key tiles it spills, and every scratch reload then
+  // waits on the in-flight loads.
   //
   // Tried and measured slower on MI355X: running the two waves that share a
   // SIMD half a tile apart (one in softmax while the other issues MFMAs,
