@@ -510,6 +510,11 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
   // SIMD half a tile apart (one in softmax while the other issues MFMAs,
   // with a ring of 3 V buffers), 700 vs 758 TFLOP/s; and two 4-wave
   // workgroups per CU instead of one 8-wave workgroup, 2.6x slower.
+  // Four waves of 64 query rows each (one wave per SIMD, so each K or V
+  // operand read from LDS feeds two MFMAs and 512 registers are available)
+  // was correct but ran at 141 TFLOP/s: the compiler keeps the score
+  // accumulators in AGPRs, copies them through VGPRs for the softmax and
+  // spills the staging state to scratch.
   stage_t R;
   load_tile(0, R);
   store_tile(0, 0, R);
