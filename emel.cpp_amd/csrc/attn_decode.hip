@@ -23,8 +23,9 @@
 // q8_0 pools: identical structure; for scores the 16 int8 values of a lane
 // are turned into exact fp16 (biased by a constant that the dot product's
 // start value removes) with byte permutes, and the lane's block scale
-// multiplies its partial score; for P.V the int8 values
-// go to fp32 and the token scale folds into an fp32 weight p * d_v.
+// multiplies its partial score; for P.V the int8 values of two tokens
+// become exact fp16 pairs and the token scale folds into the fp16 weight
+// p * d_v.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -86,14 +87,26 @@ __device__ __forceinline__ void i8x16_to_half_biased(const uint4_t w, half2_t ou
   }
 }
 
-// 16 int8 -> 16 fp32 values q + 128 (exact; one v_cvt_f32_ubyte each).
-__device__ __forceinline__ void u8x16_biased_to_float(const uint4_t w, float out[16]) {
-  const uint32_t ws[4] = {w.x ^ 0x80808080u, w.y ^ 0x80808080u, w.z ^ 0x80808080u,
-                          w.w ^ 0x80808080u};
+// Two rows of 16 int8 (tokens t0, t1, same dims) -> 16 half2 pairs
+// (q_t0[i], q_t1[i]), exact: one permute interleaves two dims of both
+// tokens, two permutes put each byte (biased by +128) under the fp16
+// exponent of 1024, and a packed fp16 add of -1152 leaves q exactly.
+__device__ __forceinline__ void i8x16_pair_to_half2(const uint4_t w0, const uint4_t w1,
+                                                    half2_t out[16]) {
+  const uint32_t a[4] = {w0.x ^ 0x80808080u, w0.y ^ 0x80808080u, w0.z ^ 0x80808080u,
+                         w0.w ^ 0x80808080u};
+  const uint32_t b[4] = {w1.x ^ 0x80808080u, w1.y ^ 0x80808080u, w1.z ^ 0x80808080u,
+                         w1.w ^ 0x80808080u};
+  const half2_t bias = as_half2(0xE480E480u);  // (-1152, -1152)
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-#pragma unroll
-    for (int b = 0; b < 4; ++b) out[4 * i + b] = static_cast<float>((ws[i] >> (8 * b)) & 0xFFu);
+    // bytes (a0, b0, a1, b1) and (a2, b2, a3, b3)
+    const uint32_t lo = __builtin_amdgcn_perm(b[i], a[i], 0x05010400u);
+    const uint32_t hi = __builtin_amdgcn_perm(b[i], a[i], 0x07030602u);
+    out[4 * i + 0] = as_half2(__builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u)) + bias;
+    out[4 * i + 1] = as_half2(__builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u)) + bias;
+    out[4 * i + 2] = as_half2(__builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u)) + bias;
+    out[4 * i + 3] = as_half2(__builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u)) + bias;
   }
 }
 
@@ -185,7 +198,6 @@ struct decode_state {
   float m[G];        // reference max (log2 domain, scale folded in)
   float l[G];
   float acc[G][16];
-  float corr[G];     // q8_0: sum of P.V weights (undoes the +128 byte bias)
   float kbias[G];    // q8_0: -1152 * sum of the lane's 16 q values (K byte bias)
 };
 
@@ -226,12 +238,11 @@ __device__ __forceinline__ void consume_tile(decode_state<D, G, Q8> &S, const ti
     }
   }
 
-  // V operands: f16 pools pair the two tokens per dimension for
-  // v_dot2_f32_f16 with the fp16 pair (p0, p1); q8_0 pools keep the bytes
-  // biased by +128 (exact in fp32 via v_cvt_f32_ubyte) and fold the token
-  // scale into an fp32 weight, so nothing on the q8_0 P.V path is rounded.
+  // V operands: both pools pair the two tokens per dimension for
+  // v_dot2_f32_f16: f16 pools with the fp16 pair (p0, p1), q8_0 pools with
+  // the exact fp16 q values and the pair (p0 * d_v0, p1 * d_v1).
   [[maybe_unused]] half2_t vlo[8], vhi[8];
-  [[maybe_unused]] float vf0[16], vf1[16];
+  [[maybe_unused]] half2_t vq[16];
   [[maybe_unused]] float vs0 = 1.0f, vs1 = 1.0f;
   if constexpr (!Q8) {
     const uint32_t w0[8] = {T.v0.a.x, T.v0.a.y, T.v0.a.z, T.v0.a.w,
@@ -244,8 +255,7 @@ __device__ __forceinline__ void consume_tile(decode_state<D, G, Q8> &S, const ti
       vhi[j] = as_half2(__builtin_amdgcn_perm(w1[j], w0[j], 0x07060302u));
     }
   } else {
-    u8x16_biased_to_float(T.v0.a, vf0);
-    u8x16_biased_to_float(T.v1.a, vf1);
+    i8x16_pair_to_half2(T.v0.a, T.v1.a, vq);
     vs0 = f16_bits_to_f32(static_cast<uint16_t>(T.v0.d));
     vs1 = f16_bits_to_f32(static_cast<uint16_t>(T.v1.d));
   }
@@ -257,7 +267,6 @@ __device__ __forceinline__ void consume_tile(decode_state<D, G, Q8> &S, const ti
       const float alpha = fast_exp2(S.m[h] - mx);  // 0 on the first valid token
       S.m[h] = mx;
       S.l[h] *= alpha;
-      if constexpr (Q8) S.corr[h] *= alpha;
 #pragma unroll
       for (int i = 0; i < 16; ++i) S.acc[h][i] *= alpha;
     }
@@ -269,11 +278,12 @@ __device__ __forceinline__ void consume_tile(decode_state<D, G, Q8> &S, const ti
     }
     S.l[h] += p0 + p1;
     if constexpr (Q8) {
-      const float w0 = p0 * vs0;
-      const float w1 = p1 * vs1;
-      S.corr[h] += w0 + w1;
+      // fp16 weights p * d_v (the f16 route rounds p to fp16 the same way);
+      // measured 5.14 TB/s against 4.85 for fp32 FMAs of p * d_v with the
+      // bytes converted to fp32, at the Llama-3-8B q8_0 shape
+      const half2_t ww = pack_half2(p0 * vs0, p1 * vs1);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) S.acc[h][i] = fmaf(w1, vf1[i], fmaf(w0, vf0[i], S.acc[h][i]));
+      for (int i = 0; i < 16; ++i) S.acc[h][i] = dot2(ww, vq[i], S.acc[h][i]);
     } else {
       const half2_t pp = pack_half2(p0, p1);
 #pragma unroll
@@ -373,7 +383,6 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
     S.kbias[h] = -1152.0f * qsum;
     S.m[h] = -INFINITY;
     S.l[h] = 0.0f;
-    S.corr[h] = 0.0f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) S.acc[h][i] = 0.0f;
   }
@@ -475,15 +484,6 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
     bool o0, o1;
     load_tile(base, T, o0, o1);
     consume_tile<D, G, Q8, true>(S, T, o0, o1, P.c);
-  }
-
-  if constexpr (Q8) {
-    // acc holds sum w * (q + 128): remove the bias term
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) S.acc[h][i] = fmaf(-128.0f, S.corr[h], S.acc[h][i]);
-    }
   }
 
   // merge the token groups of the wave (lane bits >= log2(LPT))
