@@ -154,7 +154,7 @@ class Scenario:
             out[s] = oracle.attention_f64(q[s], k, v, self.n_head, self.n_kv, self.D, n, scale)
         return out
 
-    def gpu_decode(self, layer, q, lens=None, scale=None):
+    def gpu_decode(self, layer, q, lens=None, scale=None, ws=None):
         torch = self.torch
         lens = self.lens if lens is None else lens
         scale = (1.0 / np.sqrt(self.D)) if scale is None else scale
@@ -163,8 +163,9 @@ class Scenario:
         out = torch.full_like(qd, float("nan"))
         kl = torch.tensor(lens, dtype=torch.int32, device=self.device)
         mx = max(lens)
-        ws = torch.empty(emelk.decode_workspace_bytes(self.g, self.n_seq, mx) // 4 + 1,
-                         dtype=torch.float32, device=self.device)
+        if ws is None:
+            ws = torch.zeros(emelk.decode_workspace_bytes(self.g, self.n_seq, mx) // 4 + 1,
+                             dtype=torch.float32, device=self.device)
         emelk.decode(self.g, self.k_pool, self.v_pool, layer, qd, out, kl, mx, self.tables,
                      float(scale), ws)
         torch.cuda.synchronize()

@@ -252,6 +252,30 @@ def test_decode_edge_shapes(device, n_head, n_kv, D, bt, lens, kv_type):
     _decode_case(sc, 0, 500 + sum(lens))
 
 
+def test_decode_reused_workspace_across_shapes(device):
+    """One workspace across calls whose split plans differ (other lengths and
+    maximum length): every call matches the oracle, and repeating a call
+    gives bit-identical output (the split merge has a fixed order)."""
+    import torch
+    banner("decode: one workspace, several shapes")
+    lens = [3001, 700, 33, 1]
+    sc = Scenario(n_layer=1, n_head=32, n_kv=8, head_dim=128, block_tokens=32, lens=lens,
+                  seed=77)
+    ws = torch.full((emelk.decode_workspace_bytes(sc.g, len(lens), max(lens)) // 4 + 1,),
+                    float("nan"), dtype=torch.float32, device=device)
+    rng = np.random.default_rng(78)
+    q = rng.standard_normal((len(lens), 32 * 128)).astype(np.float32)
+    scale = 1.0 / np.sqrt(128)
+    first = None
+    for i, ls in enumerate([lens, [64, 700, 1, 2], [1500, 1, 1, 1], lens]):
+        got = sc.gpu_decode(0, q, lens=ls, ws=ws)
+        assert_close(got, sc.oracle_decode(0, q, lens=ls, scale=scale),
+                     what=f"call {i} lens {ls}")
+        if i == 0:
+            first = got
+    assert np.array_equal(got.view(np.uint32), first.view(np.uint32))
+
+
 def test_decode_step_append_then_attend(device):
     # One decode step as the generator runs it: allocate_slots(1) per
     # sequence, append the new token at position len, attend over len+1.
@@ -430,7 +454,7 @@ def test_decode_graph_replay_matches_eager(device):
     newv = torch.randn(2, 1, 1024, device=device)
     q = torch.randn(2, 32, 128, device=device)
     out = torch.zeros_like(q)
-    ws = torch.empty(emelk.decode_workspace_bytes(sc.g, 2, 3001) // 4 + 1, device=device)
+    ws = torch.zeros(emelk.decode_workspace_bytes(sc.g, 2, 3001) // 4 + 1, device=device)
 
     def run():
         emelk.append(sc.g, sc.k_pool, sc.v_pool, 0, newk, newv, pos, sc.tables)
