@@ -514,7 +514,10 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
   // operand read from LDS feeds two MFMAs and 512 registers are available)
   // was correct but ran at 141 TFLOP/s: the compiler keeps the score
   // accumulators in AGPRs, copies them through VGPRs for the softmax and
-  // spills the staging state to scratch.
+  // spills the staging state to scratch.  With 32-key tiles it compiles
+  // without spills but runs at 529 vs 823 TFLOP/s: one wave per SIMD leaves
+  // nothing to issue MFMAs while a wave is in its softmax, and the
+  // accumulators still move between AGPRs and VGPRs on every tile.
   stage_t R;
   load_tile(0, R);
   store_tile(0, 0, R);
