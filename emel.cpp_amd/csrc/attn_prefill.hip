@@ -518,6 +518,10 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
   // without spills but runs at 529 vs 823 TFLOP/s: one wave per SIMD leaves
   // nothing to issue MFMAs while a wave is in its softmax, and the
   // accumulators still move between AGPRs and VGPRs on every tile.
+  // Staging V key-major (16-byte stores, no register transpose) and reading
+  // the P.V operand with LDS transpose loads (ds_read_b64_tr_b16, two per
+  // operand) was correct but slower: 779 vs 824 TFLOP/s with rows padded to
+  // D + 32 halves, 736 with D + 8.
   stage_t R;
   load_tile(0, R);
   store_tile(0, 0, R);
