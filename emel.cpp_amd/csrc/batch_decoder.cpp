@@ -74,6 +74,9 @@ extern "C" emel_error_type emelk_batch_decoder_create(const emelk_kv_geometry *g
       emelk_rope_table_positions(rope) < max_kv_len) {
     return EMELK_ERR_INVALID_REQUEST;
   }
+  // page copies of the tail split run on the cache's stream; the decoder's
+  // kernels must be ordered after them (and the copies after earlier appends)
+  if (stream != emelk_kv_cache_stream(cache)) return EMELK_ERR_INVALID_REQUEST;
   const int32_t stride = (max_kv_len + g->block_tokens - 1) / g->block_tokens;
   if (stride > EMELK_MAX_BLOCKS_PER_SEQUENCE) return EMELK_ERR_INVALID_REQUEST;
   uint64_t ws = 0;

@@ -362,6 +362,9 @@ extern "C" void emelk_kv_cache_destroy(emelk_kv_cache *c) {
 
 extern "C" void *emelk_kv_cache_k_pool(emelk_kv_cache *c) { return c ? c->k_pool : nullptr; }
 extern "C" void *emelk_kv_cache_v_pool(emelk_kv_cache *c) { return c ? c->v_pool : nullptr; }
+extern "C" void *emelk_kv_cache_stream(const emelk_kv_cache *c) {
+  return c ? static_cast<void *>(c->stream) : nullptr;
+}
 
 // allocate_slots::copy_block_fn target (text/generator/context.hpp:36-50 ->
 // copy_attention_kv_block, detail.hpp:3334-3417): validates the request like

@@ -209,6 +209,7 @@ _SIGNATURES = [
     ("emelk_kv_cache_destroy", None, [_P]),
     ("emelk_kv_cache_k_pool", _P, [_P]),
     ("emelk_kv_cache_v_pool", _P, [_P]),
+    ("emelk_kv_cache_stream", _P, [_P]),
     ("emelk_kv_cache_copy_block", ctypes.c_bool,
      [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _P, c_i32p]),
     ("emelk_build_info", ctypes.c_char_p, []),

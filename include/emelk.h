@@ -330,6 +330,8 @@ emel_error_type emelk_kv_cache_create(const emelk_kv_geometry *g, void *stream,
 void emelk_kv_cache_destroy(emelk_kv_cache *cache);
 void *emelk_kv_cache_k_pool(emelk_kv_cache *cache);
 void *emelk_kv_cache_v_pool(emelk_kv_cache *cache);
+/* The stream the cache was created with (its page copies run there). */
+void *emelk_kv_cache_stream(const emelk_kv_cache *cache);
 /* emelk_copy_block_fn: user_data is an emelk_kv_cache*.  Enqueues the copy of
  * one page (all layers, K and V) on the cache's stream. */
 bool emelk_kv_cache_copy_block(int32_t src_block, int32_t dst_block, int32_t block_tokens,

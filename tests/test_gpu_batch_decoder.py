@@ -129,3 +129,21 @@ def test_batch_decoder_step_is_all_or_nothing(device):
     assert emelk.lib.emelk_kv_sequence_length(actor.handle, 1) == 48
     assert emelk.lib.emelk_kv_free_count(actor.handle) == free_before
     dec.close()
+
+
+def test_batch_decoder_requires_the_cache_stream(device):
+    """Tail-split page copies run on the cache's stream, so a decoder on any
+    other stream would race them: creation is refused."""
+    import torch
+    banner("batch decoder: stream must be the cache's")
+    g = emelk.geometry(1, H, HKV, D, BT, 8, emelk.KV_F16)
+    actor = emelk.KvActor()
+    assert actor.reserve(2, 8, BT)[0]
+    cache = emelk.KvCache(g)
+    rope = emelk.RopeTable(D, D, 64, BASE)
+    other = torch.cuda.Stream()
+    assert (emelk.lib.emelk_kv_cache_stream(cache.handle) or 0) == \
+        torch.cuda.current_stream().cuda_stream
+    with pytest.raises(RuntimeError):
+        emelk.BatchDecoder(g, actor, cache, rope, max_batch=2, max_kv_len=64,
+                           stream=other.cuda_stream)
