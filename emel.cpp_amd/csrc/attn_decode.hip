@@ -244,11 +244,21 @@ __device__ __forceinline__ void consume_tile(decode_state<D, G, Q8> &S, const ti
   [[maybe_unused]] half2_t vlo[8], vhi[8];
   [[maybe_unused]] half2_t vq[16];
   [[maybe_unused]] float vs0 = 1.0f, vs1 = 1.0f;
+  // Masked tokens (past the end, invalid page) were read from a clamped
+  // address that may hold never-written bytes: their V words and scales are
+  // zeroed, since p = 0 times a NaN slot would still be NaN.
   if constexpr (!Q8) {
-    const uint32_t w0[8] = {T.v0.a.x, T.v0.a.y, T.v0.a.z, T.v0.a.w,
-                            T.v0.b.x, T.v0.b.y, T.v0.b.z, T.v0.b.w};
-    const uint32_t w1[8] = {T.v1.a.x, T.v1.a.y, T.v1.a.z, T.v1.a.w,
-                            T.v1.b.x, T.v1.b.y, T.v1.b.z, T.v1.b.w};
+    uint32_t w0[8] = {T.v0.a.x, T.v0.a.y, T.v0.a.z, T.v0.a.w,
+                      T.v0.b.x, T.v0.b.y, T.v0.b.z, T.v0.b.w};
+    uint32_t w1[8] = {T.v1.a.x, T.v1.a.y, T.v1.a.z, T.v1.a.w,
+                      T.v1.b.x, T.v1.b.y, T.v1.b.z, T.v1.b.w};
+    if constexpr (MASKED) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        w0[j] = ok0 ? w0[j] : 0u;
+        w1[j] = ok1 ? w1[j] : 0u;
+      }
+    }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       vlo[j] = as_half2(__builtin_amdgcn_perm(w1[j], w0[j], 0x05040100u));
@@ -258,6 +268,10 @@ __device__ __forceinline__ void consume_tile(decode_state<D, G, Q8> &S, const ti
     i8x16_pair_to_half2(T.v0.a, T.v1.a, vq);
     vs0 = f16_bits_to_f32(static_cast<uint16_t>(T.v0.d));
     vs1 = f16_bits_to_f32(static_cast<uint16_t>(T.v1.d));
+    if constexpr (MASKED) {  // the int8 values are always finite
+      vs0 = ok0 ? vs0 : 0.0f;
+      vs1 = ok1 ? vs1 : 0.0f;
+    }
   }
 
 #pragma unroll

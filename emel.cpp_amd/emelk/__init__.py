@@ -443,6 +443,7 @@ class RopeTable:
 
     def __init__(self, n_rot, head_dim, max_positions, freq_base, pairing=NORMAL_PAIRING,
                  stream=None):
+        self.handle = None
         self.params = RopeParams(n_rot, *pairing, freq_base)
         h = ctypes.c_void_p(None)
         _check(lib.emelk_rope_table_create(ctypes.byref(self.params), head_dim, max_positions,
@@ -476,6 +477,7 @@ class KvCache:
     """Device pools owned by the library (emelk_kv_cache_create)."""
 
     def __init__(self, g, stream=None):
+        self.handle = None
         self.g = g
         h = ctypes.c_void_p(None)
         _check(lib.emelk_kv_cache_create(ctypes.byref(g), _stream(stream), ctypes.byref(h)),
@@ -503,6 +505,7 @@ class BatchDecoder:
 
     def __init__(self, g, actor: "KvActor", cache: KvCache, rope: RopeTable, max_batch,
                  max_kv_len, stream=None):
+        self.handle = None  # set only once creation succeeds (close() checks it)
         self._keep = (actor, cache, rope)
         h = ctypes.c_void_p(None)
         _check(lib.emelk_batch_decoder_create(ctypes.byref(g), actor.handle, cache.handle,

@@ -437,6 +437,43 @@ def test_decode_masks_invalid_pages_and_short_tables(device):
                  what="short table")
 
 
+@pytest.mark.parametrize("kv_type,n_head,n_kv,D,bt,lens", [
+    (emelk.KV_F16, 32, 8, 128, 32, [300, 1000, 37, 1]),
+    (emelk.KV_F16, 32, 8, 64, 16, [301, 77, 5]),
+    (emelk.KV_F16, 8, 8, 128, 12, [100, 29]),       # block_tokens not a multiple of 8
+    (emelk.KV_Q8_0, 32, 8, 128, 32, [300, 1000, 37, 1]),
+    (emelk.KV_Q8_0, 16, 8, 128, 16, [333, 18]),
+])
+def test_decode_never_uses_unwritten_slots(device, kv_type, n_head, n_kv, D, bt, lens):
+    """The pool starts as 0xFF bytes (NaN in every never-written f16 slot and
+    q8_0 scale): masked tokens past a sequence's end, and tokens on an invalid
+    page, must contribute nothing, not 0 * NaN."""
+    banner(f"decode over a NaN-filled pool type={kv_type} H={n_head}/{n_kv} D={D} bt={bt} "
+           f"lens={lens}")
+    import torch
+    sc = Scenario(n_layer=1, n_head=n_head, n_kv=n_kv, head_dim=D, block_tokens=bt, lens=lens,
+                  seed=sum(lens) + D, kv_type=kv_type, pool_byte=0xFF)
+    q = np.random.default_rng(9).standard_normal((sc.n_seq, n_head * D)).astype(np.float32)
+    got = sc.gpu_decode(0, q)
+    assert_close(got, sc.oracle_decode(0, q), what="NaN-filled pool")
+    # an invalid page in the middle of sequence 0: its tokens are left out
+    t = sc.tables_host.copy()
+    t[0, 1] = 0xFFFF
+    sc.tables = torch.from_numpy(np.ascontiguousarray(t).view(np.int16)).to(device)
+    got = sc.gpu_decode(0, q)
+    n = lens[0]
+    keep = np.array([p // bt != 1 for p in range(n)])
+    if kv_type == emelk.KV_F16:
+        stored = lambda r: oracle.fp16_to_fp32(oracle.fp32_to_fp16(r))  # noqa: E731
+    else:
+        stored = lambda r: oracle.dequantize_q8_0(oracle.quantize_q8_0(r))  # noqa: E731
+    k = stored(sc.k_rows[0][0])[keep]
+    v = stored(sc.v_rows[0][0])[keep]
+    want = oracle.attention_f64(oracle.fp16_to_fp32(oracle.fp32_to_fp16(q[0])), k, v, n_head,
+                                n_kv, D, int(keep.sum()), 1 / np.sqrt(D))
+    assert_close(got[0], want, what="NaN-filled pool, invalid page")
+
+
 def test_decode_graph_replay_matches_eager(device):
     # One layer's append + decode captured in a HIP graph and replayed with
     # eager work and synchronisations in between: every replay must equal
