@@ -47,6 +47,13 @@ constexpr int k_max_split_pages = 1024;
 // spill; a read-only walk of the same 64 KiB pages tops out at 6.76 TB/s,
 // which 2 sets already reach within 5%.
 constexpr int k_decode_nb = 2;
+// q8_0 at head_dim 128 was also built with scores on MFMA
+// (v_mfma_f32_16x16x32_f16 with rows = (32-value block, head), so the int8
+// values enter exactly and each lane scales its own block): correct, 15%
+// fewer VALU instructions, but no faster (5.23 vs 5.20 TB/s) and no faster
+// with 3 or 4 tile sets in flight; the shuffles that sum the blocks and hand
+// P to the V lanes lengthen each tile's dependent chain.  Scaling K to fp16
+// before the MFMA instead breaks the 2e-3 bar on the x20-outlier data.
 
 // Waves per workgroup = KV heads per workgroup: min(n_head_kv, 8) when it
 // divides n_head_kv, else 1.

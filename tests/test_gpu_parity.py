@@ -244,6 +244,8 @@ def test_decode_config4_q8_0(device):
     (4, 2, 128, 32, [64, 65, 2047, 2048, 2049], emelk.KV_F16),    # tile/split edges
     (4, 2, 128, 32, [1, 33, 4097], emelk.KV_Q8_0),
     (16, 8, 128, 16, [1000], emelk.KV_Q8_0),                      # G=2 q8_0
+    (8, 1, 128, 32, [129, 1000, 16], emelk.KV_Q8_0),              # G=8 q8_0
+    (4, 4, 128, 12, [100, 7], emelk.KV_Q8_0),                     # G=1, pages not a multiple of 8
 ])
 def test_decode_edge_shapes(device, n_head, n_kv, D, bt, lens, kv_type):
     banner(f"decode edges H={n_head} HK={n_kv} D={D} bt={bt} lens={lens} type={kv_type}")
