@@ -522,6 +522,10 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
   // the P.V operand with LDS transpose loads (ds_read_b64_tr_b16, two per
   // operand) was correct but slower: 779 vs 824 TFLOP/s with rows padded to
   // D + 32 halves, 736 with D + 8.
+  // A software pipeline with 32-key tiles (tile t+1's scores computed in the
+  // same stretch as tile t's softmax, K staged two tiles ahead, a ring of 3
+  // V buffers, 228 VGPRs): 812 vs 826 TFLOP/s, and 790 with the K reads and
+  // MFMAs explicitly interleaved into the softmax (sched_group_barrier).
   stage_t R;
   load_tile(0, R);
   store_tile(0, 0, R);
