@@ -62,6 +62,9 @@ def main():
     ap.add_argument("--config", default="llama3-8b-b64-ctx8k",
                     choices=sorted(CONFIGS) + ["llama3-8b-prefill512-evict25"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--separate-append", action="store_true",
+                    help="append with emelk_kv_append, then emelk_attn_decode (two launches per "
+                         "layer) instead of emelk_attn_decode_append")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--eager", action="store_true",
@@ -167,13 +170,22 @@ def main():
     scale = float(1.0 / np.sqrt(D))
     stream = torch.cuda.current_stream()
 
+    new_k2 = [t.view(B, HK * D) for t in new_k]
+    new_v2 = [t.view(B, HK * D) for t in new_v]
+
     def step(events=None):
         for layer in range(L):
-            emelk.append(g, k_pool, v_pool, layer, new_k[layer], new_v[layer], positions, tables)
+            if args.separate_append:
+                emelk.append(g, k_pool, v_pool, layer, new_k[layer], new_v[layer], positions,
+                             tables)
             if events is not None:
                 events[layer][0].record(stream)
-            emelk.decode(g, k_pool, v_pool, layer, q[layer], out[layer], kv_lens, max_len, tables,
-                         scale, ws)
+            if args.separate_append:
+                emelk.decode(g, k_pool, v_pool, layer, q[layer], out[layer], kv_lens, max_len,
+                             tables, scale, ws)
+            else:  # the step's store of the new token and its attention in one launch
+                emelk.decode_append(g, k_pool, v_pool, layer, new_k2[layer], new_v2[layer],
+                                    q[layer], out[layer], kv_lens, max_len, tables, scale, ws)
             if events is not None:
                 events[layer][1].record(stream)
 
@@ -182,7 +194,8 @@ def main():
     torch.cuda.synchronize()
 
     # Kernel timing: eager launches with HIP events around each layer's
-    # decode call (decode_kernel + combine_kernel) on the stream they run on.
+    # decode call (decode_kernel, with the new token's store unless --separate-append, +
+    # combine_kernel) on the stream they run on.
     K = args.steps
     ev = [[[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)]
            for _ in range(L)] for _ in range(K)]
@@ -229,6 +242,8 @@ def main():
     step_kv_bytes = kv_read_layer * L
     step_bytes = (kv_read_layer + q_bytes + o_bytes + table_bytes + append_bytes) * L
     kernel_bytes = kv_read_layer + q_bytes + o_bytes + table_bytes
+    if not args.separate_append:  # the decode launch also stores the new token
+        kernel_bytes += append_bytes
     kv_gbs = step_kv_bytes / (ms_per_step * 1e-3) / 1e9
     achieved = kernel_bytes / (attn_avg_ms * 1e-3) / 1e9
 
@@ -288,7 +303,10 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": PMC_TRAFFIC_BYTES.get(args.config),
-                     "kernel": "decode_kernel + combine_kernel (HIP events per layer call)",
+                     "kernel": ("decode_kernel + combine_kernel (HIP events per layer call)"
+                                if args.separate_append else
+                                "decode_kernel with the fused append + combine_kernel (HIP events "
+                                "per layer call)"),
                      "bytes_per_launch": kernel_bytes, "avg_launch_ms": round(attn_avg_ms, 4)},
         "cpu_baseline": cpu,
         "parity_full_size": parity,

@@ -78,7 +78,15 @@ struct decode_params {
   int32_t max_splits;
   float *part_acc;  // [n_seq][n_head][max_splits][D]
   float *part_ml;   // [n_seq][n_head][max_splits][2]
+  // Fused append (null new_k: none): the token at position kv_lens - 1 of
+  // each sequence, rows new_k/new_v fp32 [n_seq][n_head_kv][D], is stored
+  // into k_wr/v_wr (the same pools) and attended from registers.
+  const float *new_k;
+  const float *new_v;
+  uint8_t *k_wr;
+  uint8_t *v_wr;
 };
+
 
 // 16 int8 -> 8 half2 holding b + 1152 exactly: byte b becomes the fp16 bit
 // pattern 0x64XX with XX = b + 128, whose value is 1024 + b + 128.  The
@@ -176,6 +184,50 @@ __device__ __forceinline__ void load_row_uniform(const uint8_t *__restrict__ reg
     r.a = load16_stream(u + lane_off);
     const uint8_t *s = region + static_cast<uint32_t>(bt) * D + static_cast<uint32_t>(row0) * (D / 16);
     r.d = load2_stream(s + lane_sc_off);
+  }
+}
+
+// The stored form of one new row, in the lane layout of row_regs: f16 pools
+// round to fp16 (fp32_to_fp16, kernel/detail.hpp:372-392); q8_0 pools
+// quantize each 32-value block as quantize_row_q8_0_strided
+// (kernel/detail.hpp:804-824), the two lanes of a block sharing its amax.
+template <int D, bool Q8>
+__device__ __forceinline__ void new_row_regs(const float *__restrict__ row, int32_t lane_in_row,
+                                             row_regs<D, Q8> &r) {
+  if constexpr (!Q8) {
+    const float4_t a0 = *reinterpret_cast<const float4_t *>(row + 8 * lane_in_row);
+    const float4_t a1 = *reinterpret_cast<const float4_t *>(row + 8 * lane_in_row + 4);
+    const float4_t b0 = *reinterpret_cast<const float4_t *>(row + D / 2 + 8 * lane_in_row);
+    const float4_t b1 = *reinterpret_cast<const float4_t *>(row + D / 2 + 8 * lane_in_row + 4);
+    r.a = uint4_t{as_u32(pack_half2(a0.x, a0.y)), as_u32(pack_half2(a0.z, a0.w)),
+                  as_u32(pack_half2(a1.x, a1.y)), as_u32(pack_half2(a1.z, a1.w))};
+    r.b = uint4_t{as_u32(pack_half2(b0.x, b0.y)), as_u32(pack_half2(b0.z, b0.w)),
+                  as_u32(pack_half2(b1.x, b1.y)), as_u32(pack_half2(b1.z, b1.w))};
+  } else {
+    float v[16];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float4_t f = *reinterpret_cast<const float4_t *>(row + 16 * lane_in_row + 4 * j);
+      v[4 * j + 0] = f.x;
+      v[4 * j + 1] = f.y;
+      v[4 * j + 2] = f.z;
+      v[4 * j + 3] = f.w;
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) amax = fmaxf(amax, fabsf(v[j]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, k_wave));  // the other half of the block
+    const float d = amax / 127.0f;
+    const float inv_d = d != 0.0f ? 1.0f / d : 0.0f;
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      int q = static_cast<int>(roundf(v[j] * inv_d));
+      q = q < -127 ? -127 : (q > 127 ? 127 : q);
+      w[j / 4] |= (static_cast<uint32_t>(q) & 0xFFu) << (8 * (j % 4));
+    }
+    r.a = uint4_t{w[0], w[1], w[2], w[3]};
+    r.d = f32_to_f16_bits(d);
   }
 }
 
@@ -373,7 +425,7 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
     pg[k] = (i < max_pages && lb < P.table_stride) ? table[lb] : 0xFFFFFFFFu;
   }
   if (start >= len) return;  // uniform; the combine kernel never reads this split
-  const int32_t end = min(len, start + P.tokens_per_split);
+  int32_t end = min(len, start + P.tokens_per_split);  // lowered to the new token's position when fused
   const int32_t n_pages = (end - 1) / bt - first_page + 1;  // <= max_pages
 
   int bad = 0;
@@ -418,6 +470,48 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
       static_cast<uint32_t>(grp) * (Q8 ? D : 2 * D) + static_cast<uint32_t>(lane_in_row) * 16u;
   const uint32_t lane_sc_off =
       static_cast<uint32_t>(grp) * (D / 16) + static_cast<uint32_t>(lane_in_row / 2) * 2u;
+
+  // Fused append: the workgroup whose split holds position len - 1 stores
+  // the new token and attends to it from registers after the memory tiles
+  // (so nothing reads it back); the memory path ends before it.
+  [[maybe_unused]] tile_regs<D, Q8> TN;
+  bool has_new = false;
+  bool new_ok = false;
+  if (P.new_k != nullptr && len - 1 >= start && len - 1 < end) {  // uniform
+    const int32_t p = len - 1;
+    has_new = true;
+    end = p;
+    const uint32_t page = s_pages[p / bt - first_page];
+    new_ok = page != 0xFFFFFFFFu;
+    const uint64_t row = (static_cast<uint64_t>(seq) * P.L.n_head_kv + kvh) * D;
+    new_row_regs<D, Q8>(P.new_k + row, lane_in_row, TN.k0);
+    new_row_regs<D, Q8>(P.new_v + row, lane_in_row, TN.v0);
+    TN.k1 = TN.k0;
+    TN.v1 = TN.v0;
+    if (new_ok && grp == 0) {
+      const uint64_t region = static_cast<uint64_t>(P.layer) * P.L.layer_bytes +
+                              static_cast<uint64_t>(kvh) * P.L.region_bytes +
+                              static_cast<uint64_t>(page) * page_bytes;
+      const int32_t off = p % bt;
+#pragma unroll
+      for (int kv = 0; kv < 2; ++kv) {
+        uint8_t *reg = (kv == 0 ? P.k_wr : P.v_wr) + region;
+        const row_regs<D, Q8> &r = kv == 0 ? TN.k0 : TN.v0;
+        if constexpr (!Q8) {
+          uint8_t *dst = reg + static_cast<uint64_t>(off) * D * 2u + lane_in_row * 16u;
+          store16(dst, r.a);
+          store16(dst + D, r.b);
+        } else {
+          store16(reg + static_cast<uint64_t>(off) * D + lane_in_row * 16u, r.a);
+          if ((lane_in_row & 1) == 0) {
+            reinterpret_cast<uint16_t *>(reg + static_cast<uint64_t>(bt) * D)
+                [static_cast<uint64_t>(off) * (D / 32) + lane_in_row / 2] =
+                    static_cast<uint16_t>(r.d);
+          }
+        }
+      }
+    }
+  }
 
   // Loads the tile at `tbase` (rows past `end` and rows on invalid pages
   // read a valid clamped address and are reported in ok0/ok1).
@@ -506,6 +600,7 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
     load_tile(base, T, o0, o1);
     consume_tile<D, G, Q8, true>(S, T, o0, o1, P.c);
   }
+  if (has_new) consume_tile<D, G, Q8, true>(S, TN, new_ok && grp == 0, false, P.c);
 
   // merge the token groups of the wave (lane bits >= log2(LPT))
 #pragma unroll
@@ -715,12 +810,14 @@ extern "C" emel_error_type emelk_attn_decode_workspace_size(const emelk_kv_geome
   return EMELK_ERR_NONE;
 }
 
-extern "C" emel_error_type emelk_attn_decode(const emelk_kv_geometry *g, const void *k_pool,
-                                             const void *v_pool, int32_t layer, const float *q,
-                                             float *out, int32_t n_seq, const int32_t *kv_lens,
-                                             int32_t max_kv_len, const uint16_t *block_tables,
-                                             int32_t table_stride, float scale, void *workspace,
-                                             uint64_t workspace_bytes, void *stream) {
+namespace {
+
+emel_error_type decode_impl(const emelk_kv_geometry *g, const void *k_pool, const void *v_pool,
+                            int32_t layer, const float *q, float *out, int32_t n_seq,
+                            const int32_t *kv_lens, int32_t max_kv_len,
+                            const uint16_t *block_tables, int32_t table_stride, float scale,
+                            void *workspace, uint64_t workspace_bytes, void *stream,
+                            const float *new_k, const float *new_v) {
   emelk::pool_layout L;
   if (emelk::make_pool_layout(g, L) != EMELK_ERR_NONE || k_pool == nullptr || v_pool == nullptr ||
       q == nullptr || out == nullptr || kv_lens == nullptr || block_tables == nullptr ||
@@ -742,6 +839,10 @@ extern "C" emel_error_type emelk_attn_decode(const emelk_kv_geometry *g, const v
   P.c = scale * 1.4426950408889634f;
   P.tokens_per_split = plan.tokens_per_split;
   P.max_splits = plan.max_splits;
+  P.new_k = new_k;
+  P.new_v = new_v;
+  P.k_wr = static_cast<uint8_t *>(const_cast<void *>(k_pool));
+  P.v_wr = static_cast<uint8_t *>(const_cast<void *>(v_pool));
   const uint64_t acc_floats = static_cast<uint64_t>(n_seq) * L.n_head * plan.max_splits * L.head_dim;
   P.part_acc = static_cast<float *>(workspace);
   P.part_ml = P.part_acc + acc_floats;
@@ -767,4 +868,26 @@ extern "C" emel_error_type emelk_attn_decode(const emelk_kv_geometry *g, const v
                        kv_lens, L.n_head, plan.max_splits, plan.tokens_per_split, out);
   }
   return hipGetLastError() == hipSuccess ? EMELK_ERR_NONE : EMELK_ERR_BACKEND;
+}
+
+}  // namespace
+
+extern "C" emel_error_type emelk_attn_decode(const emelk_kv_geometry *g, const void *k_pool,
+                                             const void *v_pool, int32_t layer, const float *q,
+                                             float *out, int32_t n_seq, const int32_t *kv_lens,
+                                             int32_t max_kv_len, const uint16_t *block_tables,
+                                             int32_t table_stride, float scale, void *workspace,
+                                             uint64_t workspace_bytes, void *stream) {
+  return decode_impl(g, k_pool, v_pool, layer, q, out, n_seq, kv_lens, max_kv_len, block_tables,
+                     table_stride, scale, workspace, workspace_bytes, stream, nullptr, nullptr);
+}
+
+extern "C" emel_error_type emelk_attn_decode_append(
+    const emelk_kv_geometry *g, void *k_pool, void *v_pool, int32_t layer, const float *k_rows,
+    const float *v_rows, const float *q, float *out, int32_t n_seq, const int32_t *kv_lens,
+    int32_t max_kv_len, const uint16_t *block_tables, int32_t table_stride, float scale,
+    void *workspace, uint64_t workspace_bytes, void *stream) {
+  if (k_rows == nullptr || v_rows == nullptr) return EMELK_ERR_INVALID_REQUEST;
+  return decode_impl(g, k_pool, v_pool, layer, q, out, n_seq, kv_lens, max_kv_len, block_tables,
+                     table_stride, scale, workspace, workspace_bytes, stream, k_rows, v_rows);
 }

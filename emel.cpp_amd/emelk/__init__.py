@@ -183,6 +183,9 @@ _SIGNATURES = [
     ("emelk_attn_decode", ctypes.c_uint32,
      [ctypes.POINTER(Geometry), _P, _P, ctypes.c_int32, _P, _P, ctypes.c_int32, _P,
       ctypes.c_int32, _P, ctypes.c_int32, ctypes.c_float, _P, ctypes.c_uint64, _P]),
+    ("emelk_attn_decode_append", ctypes.c_uint32,
+     [ctypes.POINTER(Geometry), _P, _P, ctypes.c_int32, _P, _P, _P, _P, ctypes.c_int32, _P,
+      ctypes.c_int32, _P, ctypes.c_int32, ctypes.c_float, _P, ctypes.c_uint64, _P]),
     ("emelk_attn_prefill_chunk", ctypes.c_uint32,
      [ctypes.POINTER(Geometry), _P, _P, ctypes.c_int32, _P, _P, ctypes.c_int32, ctypes.c_int32,
       _P, _P, ctypes.c_int32, ctypes.c_float, _P]),
@@ -427,6 +430,19 @@ def decode(g, k_pool, v_pool, layer, q, out, kv_lens, max_kv_len, block_tables, 
                                  _ptr(block_tables), int(block_tables.shape[1]), scale,
                                  _ptr(workspace), workspace.numel() * workspace.element_size(),
                                  _stream(stream)), "emelk_attn_decode")
+
+
+def decode_append(g, k_pool, v_pool, layer, k_rows, v_rows, q, out, kv_lens, max_kv_len,
+                  block_tables, scale, workspace, stream=None):
+    """Store the token at position kv_lens - 1 (k_rows/v_rows float32
+    [n_seq, n_head_kv*head_dim]) and attend over kv_lens tokens, one launch."""
+    _check(lib.emelk_attn_decode_append(ctypes.byref(g), _ptr(k_pool), _ptr(v_pool), layer,
+                                        _ptr(k_rows), _ptr(v_rows), _ptr(q), _ptr(out),
+                                        int(q.shape[0]), _ptr(kv_lens), max_kv_len,
+                                        _ptr(block_tables), int(block_tables.shape[1]), scale,
+                                        _ptr(workspace),
+                                        workspace.numel() * workspace.element_size(),
+                                        _stream(stream)), "emelk_attn_decode_append")
 
 
 def prefill_chunk(g, k_pool, v_pool, layer, q, out, q_start, block_tables, scale, stream=None):

@@ -257,6 +257,22 @@ emel_error_type emelk_attn_decode(const emelk_kv_geometry *g, const void *k_pool
                                   int32_t n_seq, const int32_t *kv_lens, int32_t max_kv_len,
                                   const uint16_t *block_tables, int32_t table_stride, float scale,
                                   void *workspace, uint64_t workspace_bytes, void *stream);
+/* One decode step's store + attend in one launch, as
+ * compute_layer_attention_residual does per token (store_attention_kv_cache
+ * then compute_attention, text/generator/detail.hpp:3806-3840): for each
+ * sequence the token at position kv_lens[s] - 1, rows k_rows/v_rows fp32
+ * [n_seq][n_head_kv * head_dim], is written into the pools exactly as
+ * emelk_kv_append writes it (f16, or q8_0 quantized on the fly; skipped on
+ * an invalid page) and attended together with the kv_lens[s] - 1 tokens
+ * before it.  Same result as emelk_kv_append(positions = kv_lens - 1,
+ * n_tokens = 1) followed by emelk_attn_decode, up to summation order. */
+emel_error_type emelk_attn_decode_append(const emelk_kv_geometry *g, void *k_pool, void *v_pool,
+                                         int32_t layer, const float *k_rows, const float *v_rows,
+                                         const float *q, float *out, int32_t n_seq,
+                                         const int32_t *kv_lens, int32_t max_kv_len,
+                                         const uint16_t *block_tables, int32_t table_stride,
+                                         float scale, void *workspace, uint64_t workspace_bytes,
+                                         void *stream);
 
 /* Chunked-prefill attention on MFMA for one layer (f16 pools): q fp32
  * [n_seq][n_q][n_head][head_dim]; row r of sequence s attends causally to

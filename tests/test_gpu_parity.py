@@ -306,6 +306,87 @@ def test_decode_step_append_then_attend(device):
         _decode_case(sc, layer, 900 + layer)
 
 
+@pytest.mark.parametrize("kv_type,n_head,n_kv,D,bt,lens,pool_byte", [
+    (emelk.KV_F16, 32, 8, 128, 32, [95, 96, 300, 1], 0),
+    (emelk.KV_F16, 32, 8, 64, 16, [15, 16, 1000], 0xFF),
+    (emelk.KV_F16, 8, 8, 128, 12, [11, 40], 0),           # block_tokens not a multiple of 8
+    (emelk.KV_Q8_0, 32, 8, 128, 32, [31, 32, 4000], 0xFF),
+    (emelk.KV_Q8_0, 16, 8, 128, 16, [100, 1], 0),
+])
+def test_decode_append_is_append_then_decode(device, kv_type, n_head, n_kv, D, bt, lens,
+                                             pool_byte):
+    """emelk_attn_decode_append (store the token at kv_lens - 1 and attend,
+    one launch) writes the same pool bytes as emelk_kv_append and gives the
+    oracle's attention, including a new token on an invalid page."""
+    banner(f"decode_append type={kv_type} H={n_head}/{n_kv} D={D} bt={bt} lens={lens}")
+    import torch
+    sc = Scenario(n_layer=2, n_head=n_head, n_kv=n_kv, head_dim=D, block_tokens=bt, lens=lens,
+                  seed=sum(lens) + 3, extra_blocks=8, kv_type=kv_type, pool_byte=pool_byte)
+    for s in range(sc.n_seq):
+        assert sc.actor.allocate_slots(s, 1)[0]
+    sc.refresh_tables()
+    rng = np.random.default_rng(11)
+    new_k = rng.standard_normal((2, sc.n_seq, sc.kv_dim)).astype(np.float32)
+    new_v = rng.standard_normal((2, sc.n_seq, sc.kv_dim)).astype(np.float32)
+    if kv_type == emelk.KV_Q8_0:
+        new_k[np.abs(new_k) > 2.0] *= 20.0  # outliers set the block scales
+    q = rng.standard_normal((2, sc.n_seq, n_head * D)).astype(np.float32)
+    lens_now = [n + 1 for n in sc.lens]
+    kl = torch.tensor(lens_now, dtype=torch.int32, device=device)
+    mx = max(lens_now)
+    ws = torch.zeros(emelk.decode_workspace_bytes(sc.g, sc.n_seq, mx) // 4 + 1,
+                     dtype=torch.float32, device=device)
+    for layer in range(2):
+        out = torch.full((sc.n_seq, n_head, D), float("nan"), device=device)
+        emelk.decode_append(sc.g, sc.k_pool, sc.v_pool, layer,
+                            torch.from_numpy(new_k[layer]).to(device),
+                            torch.from_numpy(new_v[layer]).to(device),
+                            torch.from_numpy(q[layer]).to(device).view(sc.n_seq, n_head, D), out,
+                            kl, mx, sc.tables, float(1 / np.sqrt(D)), ws)
+        torch.cuda.synchronize()
+        for s in range(sc.n_seq):
+            sc.k_rows[layer][s] = np.concatenate([sc.k_rows[layer][s], new_k[layer][s][None]])
+            sc.v_rows[layer][s] = np.concatenate([sc.v_rows[layer][s], new_v[layer][s][None]])
+        got = out.view(sc.n_seq, -1).cpu().numpy()
+        sc.lens = list(lens_now)  # the oracle's caches place the rows up to these lengths
+        want = sc.oracle_decode(layer, q[layer], lens=lens_now)
+        assert_close(got, want, what=f"decode_append layer {layer}")
+    if pool_byte == 0:  # the oracle's pool image has zeros where nothing was written
+        for which, pool in (("k", sc.k_pool), ("v", sc.v_pool)):
+            np.testing.assert_array_equal(pool.cpu().numpy(), sc.expected_pool(which),
+                                          err_msg=f"{which} pool after decode_append")
+    # a new token on an invalid page is neither stored nor attended; the
+    # page's other tokens drop out as in decode
+    s0 = 0
+    p = sc.lens[s0]
+    t = sc.tables_host.copy()
+    t[s0, p // bt] = 0xFFFF
+    bad = torch.from_numpy(np.ascontiguousarray(t).view(np.int16)).to(device)
+    kl2 = torch.tensor([n + 1 for n in sc.lens], dtype=torch.int32, device=device)
+    ws2 = torch.zeros(emelk.decode_workspace_bytes(sc.g, sc.n_seq, mx + 1) // 4 + 1,
+                      dtype=torch.float32, device=device)
+    out = torch.full((sc.n_seq, n_head, D), float("nan"), device=device)
+    nk = torch.randn(sc.n_seq, sc.kv_dim, device=device)
+    emelk.decode_append(sc.g, sc.k_pool, sc.v_pool, 0, nk, nk.clone(),
+                        torch.from_numpy(q[0]).to(device).view(sc.n_seq, n_head, D), out, kl2,
+                        mx + 1, bad, float(1 / np.sqrt(D)), ws2)
+    torch.cuda.synchronize()
+    got = out.view(sc.n_seq, -1).cpu().numpy()
+    if kv_type == emelk.KV_F16:
+        stored = lambda r: oracle.fp16_to_fp32(oracle.fp32_to_fp16(r))  # noqa: E731
+    else:
+        stored = lambda r: oracle.dequantize_q8_0(oracle.quantize_q8_0(r))  # noqa: E731
+    keep = np.array([pos // bt != p // bt for pos in range(p)])
+    if keep.any():
+        k = stored(sc.k_rows[0][s0])[keep]
+        v = stored(sc.v_rows[0][s0])[keep]
+        want = oracle.attention_f64(oracle.fp16_to_fp32(oracle.fp32_to_fp16(q[0][s0])), k, v,
+                                    n_head, n_kv, D, int(keep.sum()), 1 / np.sqrt(D))
+        assert_close(got[s0], want, what="new token on an invalid page")
+    else:
+        assert np.all(got[s0] == 0.0)
+
+
 def test_decode_is_invariant_to_page_placement(device):
     # Same logical K/V under two different page permutations: bit-identical
     # outputs (size-independent property; run at config-3 head shape).
