@@ -39,7 +39,7 @@ HBM_PEAK_GBS = 8000.0
 # profiles/decode_kernel_llama3-8b-b64-ctx8k.md, each scaled by the same
 # counter's reading on a plain 1 GiB copy (bench.py --copy-calibration):
 # FETCH_SIZE x2.000, WRITE_SIZE x1.000.
-PMC_TRAFFIC_BYTES = {"llama3-8b-b64-ctx8k": 2158627371}
+PMC_TRAFFIC_BYTES = {"llama3-8b-b64-ctx8k": 2157387464}
 
 CONFIGS = {
     # name: (n_layer, n_head, n_kv, head_dim, block_tokens, batch, ctx, kv_type)
@@ -302,7 +302,8 @@ def main():
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": PMC_TRAFFIC_BYTES.get(args.config),
+                     "traffic": (None if args.separate_append
+                                 else PMC_TRAFFIC_BYTES.get(args.config)),
                      "kernel": ("decode_kernel + combine_kernel (HIP events per layer call)"
                                 if args.separate_append else
                                 "decode_kernel with the fused append + combine_kernel (HIP events "
