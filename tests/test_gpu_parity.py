@@ -600,3 +600,36 @@ def test_decode_graph_replay_matches_eager(device):
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"replay {i} differs"
         del scratch
+
+
+# ---- maximum sizes: a sequence spanning EMELK_MAX_BLOCKS_PER_SEQUENCE pages,
+# a batch of EMELK_MAX_SEQUENCES sequences ----
+
+@pytest.mark.parametrize("kv_type,n_head,n_kv,D,bt", [
+    (emelk.KV_F16, 8, 1, 64, 16),     # 65,536 tokens, 8 query heads per KV head
+    (emelk.KV_Q8_0, 4, 1, 128, 32),   # 131,072 tokens
+])
+def test_decode_at_the_per_sequence_page_limit(device, kv_type, n_head, n_kv, D, bt):
+    n = 4096 * bt  # EMELK_MAX_BLOCKS_PER_SEQUENCE pages
+    banner(f"decode at the page limit: {n} tokens type={kv_type} D={D} bt={bt}")
+    sc = Scenario(n_layer=1, n_head=n_head, n_kv=n_kv, head_dim=D, block_tokens=bt,
+                  lens=[n, 700], seed=61, kv_type=kv_type, outlier_frac=0.01)
+    assert -(-n // bt) == 4096
+    q = np.random.default_rng(62).standard_normal((2, n_head * D)).astype(np.float32)
+    got = sc.gpu_decode(0, q)
+    assert_close(got, sc.oracle_decode(0, q), what="decode at the page limit")
+
+
+def test_prefill_at_the_end_of_a_page_limit_sequence(device):
+    # 65,536 tokens in 4096 pages; the chunk is the last 40 rows
+    banner("prefill chunk of 40 rows after a 65,496-token prefix (4096 pages)")
+    _prefill_case(device, 8, 1, 64, 16, [65536 - 40], 40, seed=63)
+
+
+def test_decode_at_the_sequence_limit(device):
+    banner("decode of EMELK_MAX_SEQUENCES = 256 sequences, ragged")
+    lens = np.random.default_rng(64).integers(1, 300, size=256).tolist()
+    sc = Scenario(n_layer=1, n_head=8, n_kv=2, head_dim=64, block_tokens=16, lens=lens, seed=65)
+    q = np.random.default_rng(66).standard_normal((256, 8 * 64)).astype(np.float32)
+    got = sc.gpu_decode(0, q)
+    assert_close(got, sc.oracle_decode(0, q), what="256 sequences")
