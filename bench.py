@@ -75,7 +75,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the KV hot path shards by "
-                          "sequence with no exchange (see DESIGN.md); run with --gpus 1"}))
+                          "sequence with no exchange between GPUs; run with --gpus 1"}))
         sys.exit(2)
 
     import torch
