@@ -278,6 +278,10 @@ __device__ __forceinline__ void consume_tile(decode_state<D, G, Q8> &S, const ti
   to_half<D, Q8>(T.k0, kh0, ks0);
   to_half<D, Q8>(T.k1, kh1, ks1);
   float y0[G], y1[G];
+  if constexpr (Q8) {  // the softmax scale folds into each token's block scale
+    ks0 *= c;
+    ks1 *= c;
+  }
 #pragma unroll
   for (int h = 0; h < G; ++h) {
     float a = Q8 ? S.kbias[h] : 0.0f;
@@ -288,11 +292,12 @@ __device__ __forceinline__ void consume_tile(decode_state<D, G, Q8> &S, const ti
       b = dot2(S.qh[h][j], kh1[j], b);
     }
     if constexpr (Q8) {  // each lane's 16 values share one block scale
-      a *= ks0;
-      b *= ks1;
+      y0[h] = group_sum<LPT>(a * ks0);
+      y1[h] = group_sum<LPT>(b * ks1);
+    } else {
+      y0[h] = group_sum<LPT>(a) * c;
+      y1[h] = group_sum<LPT>(b) * c;
     }
-    y0[h] = group_sum<LPT>(a) * c;
-    y1[h] = group_sum<LPT>(b) * c;
     if constexpr (MASKED) {
       y0[h] = ok0 ? y0[h] : -INFINITY;
       y1[h] = ok1 ? y1[h] : -INFINITY;
