@@ -215,7 +215,18 @@ __global__ __launch_bounds__(k_threads) void copy_blocks_kernel(pool_layout L,
   const uint8_t *s = pool + L.region_offset(layer, src, 0);
   uint8_t *d = pool + L.region_offset(layer, dst, 0);
   const uint64_t n16 = L.page_bytes / 16u;
-  for (uint64_t i = threadIdx.x; i < n16; i += k_threads) store16(d + i * 16u, load16(s + i * 16u));
+  // batches of 8 loads issued before their stores keep 8 x 16 B per thread
+  // in flight
+  constexpr int kB = 8;
+  uint64_t i = threadIdx.x;
+  for (; i + (kB - 1) * k_threads < n16; i += kB * k_threads) {
+    uint4_t v[kB];
+#pragma unroll
+    for (int b = 0; b < kB; ++b) v[b] = load16(s + (i + b * k_threads) * 16u);
+#pragma unroll
+    for (int b = 0; b < kB; ++b) store16(d + (i + b * k_threads) * 16u, v[b]);
+  }
+  for (; i < n16; i += k_threads) store16(d + i * 16u, load16(s + i * 16u));
 }
 
 int grid_for(uint64_t work_items) {
