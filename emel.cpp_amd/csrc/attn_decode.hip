@@ -85,6 +85,9 @@ struct decode_params {
   const float *new_v;
   uint8_t *k_wr;
   uint8_t *v_wr;
+  // One split per sequence (max_splits == 1): the kernel writes the
+  // normalised output here and no combine kernel runs; else null.
+  float *direct_out;
 };
 
 
@@ -433,7 +436,20 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
     const int32_t lb = first_page + i;
     pg[k] = (i < max_pages && lb < P.table_stride) ? table[lb] : 0xFFFFFFFFu;
   }
-  if (start >= len) return;  // uniform; the combine kernel never reads this split
+  if (start >= len) {  // uniform; the combine kernel never reads this split
+    if (P.direct_out != nullptr && grp == 0) {  // nothing to attend: zero output
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        float *op = P.direct_out + (static_cast<uint64_t>(seq) * P.L.n_head + kvh * G + h) * D;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          *reinterpret_cast<float4_t *>(op + lane_dim<D, Q8>(lane_in_row, 4 * j)) =
+              float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+      }
+    }
+    return;
+  }
   int32_t end = min(len, start + P.tokens_per_split);  // lowered to the new token's position when fused
   const int32_t n_pages = (end - 1) / bt - first_page + 1;  // <= max_pages
 
@@ -638,6 +654,22 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
       }
       S.m[h] = mn;
     }
+  }
+  if (P.direct_out != nullptr) {  // the only split: o = acc / l
+    if (grp == 0) {
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        const float inv = S.l[h] > 0.0f ? 1.0f / S.l[h] : 0.0f;
+        float *op = P.direct_out + (static_cast<uint64_t>(seq) * P.L.n_head + kvh * G + h) * D;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          *reinterpret_cast<float4_t *>(op + lane_dim<D, Q8>(lane_in_row, 4 * j)) =
+              float4_t{S.acc[h][4 * j] * inv, S.acc[h][4 * j + 1] * inv,
+                       S.acc[h][4 * j + 2] * inv, S.acc[h][4 * j + 3] * inv};
+        }
+      }
+    }
+    return;
   }
   if (grp == 0) {
 #pragma unroll
@@ -859,6 +891,8 @@ emel_error_type decode_impl(const emelk_kv_geometry *g, const void *k_pool, cons
   P.max_splits = plan.max_splits;
   P.new_k = new_k;
   P.new_v = new_v;
+  // a single split per sequence needs no merge: the decode kernel writes out
+  P.direct_out = plan.max_splits == 1 ? out : nullptr;
   P.k_wr = static_cast<uint8_t *>(const_cast<void *>(k_pool));
   P.v_wr = static_cast<uint8_t *>(const_cast<void *>(v_pool));
   const uint64_t acc_floats = static_cast<uint64_t>(n_seq) * L.n_head * plan.max_splits * L.head_dim;
@@ -877,6 +911,7 @@ emel_error_type decode_impl(const emelk_kv_geometry *g, const void *k_pool, cons
             : emelk::dispatch_group<64, false>(group, P, grid, st);
   }
   if (!ok) return EMELK_ERR_INVALID_REQUEST;
+  if (P.direct_out != nullptr) return hipGetLastError() == hipSuccess ? EMELK_ERR_NONE : EMELK_ERR_BACKEND;
   const dim3 cgrid(n_seq * L.n_head);
   if (L.head_dim == 128) {
     hipLaunchKernelGGL(emelk::combine_kernel<128>, cgrid, dim3(128), 0, st, P.part_acc, P.part_ml,

@@ -631,5 +631,12 @@ def test_decode_at_the_sequence_limit(device):
     lens = np.random.default_rng(64).integers(1, 300, size=256).tolist()
     sc = Scenario(n_layer=1, n_head=8, n_kv=2, head_dim=64, block_tokens=16, lens=lens, seed=65)
     q = np.random.default_rng(66).standard_normal((256, 8 * 64)).astype(np.float32)
-    got = sc.gpu_decode(0, q)
+    got = sc.gpu_decode(0, q)  # one split per sequence: no combine kernel runs
     assert_close(got, sc.oracle_decode(0, q), what="256 sequences")
+    # a sequence given no token to attend gets a zero output
+    lens0 = list(lens)
+    lens0[7] = 0
+    got0 = sc.gpu_decode(0, q, lens=lens0)
+    assert np.all(got0[7] == 0.0)
+    keep = [s for s in range(256) if s != 7]
+    np.testing.assert_array_equal(got0[keep], got[keep])
