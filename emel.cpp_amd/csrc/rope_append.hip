@@ -122,14 +122,46 @@ __global__ __launch_bounds__(k_rows_per_wg *k_wave) void rope_append_kernel(rope
     for (int32_t d = 0; d < D; ++d) ss += buf[d] * buf[d];
     s_scale[wave] = 1.0f / sqrtf(ss / static_cast<float>(D) + A.eps);
   }
-  if (lane == 0 && v_norm) {
-    // apply_rms_norm_in_place (detail.hpp:1098-1106) over the token's whole v
+  if (v_norm) {  // uniform per wave
+    // apply_rms_norm_in_place (detail.hpp:1098-1106) over the token's whole
+    // v, summed in its order: the wave loads 64 values per coalesced load
+    // (8 chunks ahead) and every lane adds the squares one by one, each
+    // taken from its lane with readlane
     const float *v = A.v_rows + tok * L.n_head_kv * static_cast<uint64_t>(D);
     const int32_t n = L.n_head_kv * D;
+    constexpr int kC = 8;
     double ss = 0.0;
-    for (int32_t i = 0; i < n; ++i) ss += static_cast<double>(v[i] * v[i]);
+    for (int32_t c0 = 0; c0 < n; c0 += kC * k_wave) {
+      float sq[kC];
+#pragma unroll
+      for (int u = 0; u < kC; ++u) {
+        const int32_t i = c0 + u * k_wave + lane;
+        const float x = i < n ? v[i] : 0.0f;
+        sq[u] = x * x;
+      }
+#pragma unroll
+      for (int u = 0; u < kC; ++u) {
+        const int32_t left = n - (c0 + u * k_wave);
+        if (left <= 0) break;  // uniform
+        const double dq = static_cast<double>(sq[u]);
+        if (left >= k_wave) {  // a full chunk: lane indices known at compile time
+#pragma unroll
+          for (int j = 0; j < k_wave; ++j) {
+            const int lo = __builtin_amdgcn_readlane(static_cast<int>(__builtin_bit_cast(uint64_t, dq)), j);
+            const int hi = __builtin_amdgcn_readlane(static_cast<int>(__builtin_bit_cast(uint64_t, dq) >> 32), j);
+            ss += __builtin_bit_cast(double, (static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) |
+                                                 static_cast<uint32_t>(lo));
+          }
+        } else {
+          for (int32_t j = 0; j < left; ++j) {
+            ss += static_cast<double>(__builtin_bit_cast(
+                float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sq[u]), j)));
+          }
+        }
+      }
+    }
     const float mean = static_cast<float>(ss / static_cast<double>(n));
-    s_scale[wave] = 1.0f / sqrtf(mean + A.eps);
+    if (lane == 0) s_scale[wave] = 1.0f / sqrtf(mean + A.eps);
   }
   __syncthreads();
   if (head_norm) {

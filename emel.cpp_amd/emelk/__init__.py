@@ -251,7 +251,7 @@ class KvActor:
         self._keep = []
 
     def close(self):
-        if self.handle:
+        if self.handle and lib is not None:  # lib is None during interpreter teardown
             lib.emelk_kv_actor_destroy(self.handle)
             self.handle = None
 
@@ -468,7 +468,7 @@ class RopeTable:
         self.handle = h
 
     def close(self):
-        if self.handle:
+        if self.handle and lib is not None:  # lib is None during interpreter teardown
             lib.emelk_rope_table_destroy(self.handle)
             self.handle = None
 
@@ -507,7 +507,7 @@ class KvCache:
         return lib.emelk_kv_cache_v_pool(self.handle)
 
     def close(self):
-        if self.handle:
+        if self.handle and lib is not None:  # lib is None during interpreter teardown
             lib.emelk_kv_cache_destroy(self.handle)
             self.handle = None
 
@@ -544,7 +544,7 @@ class BatchDecoder:
                                              _ptr(out)), "emelk_batch_decoder_layer")
 
     def close(self):
-        if self.handle:
+        if self.handle and lib is not None:  # lib is None during interpreter teardown
             lib.emelk_batch_decoder_destroy(self.handle)
             self.handle = None
 
