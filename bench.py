@@ -60,7 +60,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="llama3-8b-b64-ctx8k",
-                    choices=sorted(CONFIGS) + ["llama3-8b-prefill512-evict25"])
+                    choices=sorted(CONFIGS) + ["llama3-8b-prefill512-evict25",
+                                               "llama3-8b-b64-ctx8k-generator"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--separate-append", action="store_true",
                     help="append with emelk_kv_append, then emelk_attn_decode (two launches per "
@@ -93,6 +94,8 @@ def main():
 
     if args.config == "llama3-8b-prefill512-evict25":
         return prefill_evict(args, torch, emelk, dev)
+    if args.config == "llama3-8b-b64-ctx8k-generator":
+        return generator(args, torch, emelk, dev)
     L, H, HK, D, BT, B, CTX, kvt = CONFIGS[args.config]
     kv_type = emelk.KV_F16 if kvt == "f16" else emelk.KV_Q8_0
     rng = np.random.default_rng(args.seed)
@@ -409,6 +412,83 @@ def prefill_evict(args, torch, emelk, dev):
                        "GB/s": round(copy_bytes / (copy_ms * 1e-3) / 1e9, 1),
                        "bytes": copy_bytes},
     }
+    print(json.dumps(res), flush=True)
+
+
+def generator(args, torch, emelk, dev):
+    """The multi-sequence step executor (emelk_batch_decoder) at the
+    Llama-3-8B shape: 64 sequences are prefilled to 8192 tokens through it in
+    chunks of 512 (per layer: RoPE + append, then chunked-prefill attention),
+    then each timed step extends every sequence by one token (allocate_slots
+    for the batch, block-table upload) and runs, per layer, RoPE + append and
+    decode attention.  Eager launches: a step includes host work."""
+    L, H, HK, D, BT, B, CTX = 32, 32, 8, 128, 32, 64, 8192
+    chunk = 512
+    steps = args.steps
+    max_len = CTX + args.warmup + steps + 1
+    pages = B * (-(-max_len // BT)) + 8
+    g = emelk.geometry(L, H, HK, D, BT, pages, emelk.KV_F16)
+    actor = emelk.KvActor()
+    ok, err = actor.reserve(B, pages, BT)
+    assert ok, err
+    rng = np.random.default_rng(args.seed)
+    actor.set_free_order(rng.permutation(pages).astype(np.uint16))
+    for s in range(B):
+        assert actor.allocate_sequence(s)[0]
+    cache = emelk.KvCache(g)
+    rope = emelk.RopeTable(D, D, max_len + 1, 500000.0, emelk.NORMAL_PAIRING)
+    dec = emelk.BatchDecoder(g, actor, cache, rope, max_batch=B, max_kv_len=max_len)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    ids = list(range(B))
+    scale = float(1.0 / np.sqrt(D))
+    # prefill (untimed): one set of random projections reused for every chunk and layer
+    qc = torch.randn((B, chunk, H * D), generator=gen, device=dev)
+    kc = torch.randn((B, chunk, HK * D), generator=gen, device=dev)
+    vc = torch.randn((B, chunk, HK * D), generator=gen, device=dev)
+    qr = torch.empty_like(qc)
+    oc = torch.empty_like(qc)
+    t0 = time.time()
+    for _ in range(CTX // chunk):
+        dec.begin_step(ids, chunk)
+        for layer in range(L):
+            dec.layer(layer, qc, qr, kc, vc, oc, scale)
+    torch.cuda.synchronize()
+    log(f"[bench] generator prefill of {B} x {CTX} tokens in {time.time() - t0:.1f}s")
+    del qc, kc, vc, qr, oc
+    q1 = torch.randn((B, 1, H * D), generator=gen, device=dev)
+    k1 = torch.randn((B, 1, HK * D), generator=gen, device=dev)
+    v1 = torch.randn((B, 1, HK * D), generator=gen, device=dev)
+    q1r = torch.empty_like(q1)
+    o1 = torch.empty_like(q1)
+
+    def step():
+        dec.begin_step(ids, 1)
+        for layer in range(L):
+            dec.layer(layer, q1, q1r, k1, v1, o1, scale)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ms_step = 1e3 * (time.perf_counter() - t_start) / steps
+    ctx_mean = CTX + args.warmup + (steps + 1) / 2.0
+    kv_bytes = B * ctx_mean * HK * D * 2 * 2 * L
+    res = {
+        "metric": "multi-sequence decode step through emelk_batch_decoder (tokens/s)",
+        "value": round(B / (ms_step * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+        "data": "synthetic (seeded N(0,1) projections, seeded page permutation)",
+        "config": {"workload": "llama3-8b-b64-ctx8k-generator", "n_layer": L, "batch": B,
+                   "ctx": CTX, "prefill_chunk": chunk, "step_launch": "eager",
+                   "parallelism": "single GPU"},
+        "kv_read_GBps": round(kv_bytes / (ms_step * 1e-3) / 1e9, 1),
+    }
+    dec.close()
     print(json.dumps(res), flush=True)
 
 
