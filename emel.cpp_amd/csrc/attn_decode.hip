@@ -88,6 +88,11 @@ struct decode_params {
   // One split per sequence (max_splits == 1): the kernel writes the
   // normalised output here and no combine kernel runs; else null.
   float *direct_out;
+  // Row mode (per-row chunked prefill): "sequence" v is row v % rows of
+  // sequence v / rows, attending to [0, row_q_start[v / rows] + v % rows]
+  // through that sequence's block-table row; null otherwise.
+  const int32_t *row_q_start;
+  int32_t rows;
 };
 
 
@@ -411,7 +416,10 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
   // entries are all requested before any of them is used (the page count
   // of a split is bounded by tokens_per_split, so the entries are read
   // before the length is known).
-  const int32_t len = P.kv_lens[seq];
+  const int32_t table_row = P.row_q_start != nullptr ? seq / P.rows : seq;
+  const int32_t len = P.row_q_start != nullptr
+                          ? P.row_q_start[table_row] + (seq - table_row * P.rows) + 1
+                          : P.kv_lens[seq];
   const int32_t start = split * P.tokens_per_split;
   const int32_t bt = P.L.block_tokens;
   const int32_t first_page = start / bt;
@@ -428,7 +436,7 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
   }
   constexpr int PPT = (k_max_split_pages + NT - 1) / NT;  // page entries per thread
   const int32_t max_pages = min(k_max_split_pages, P.tokens_per_split / bt + 2);
-  const uint16_t *table = P.tables + static_cast<uint64_t>(seq) * P.table_stride;
+  const uint16_t *table = P.tables + static_cast<uint64_t>(table_row) * P.table_stride;
   uint32_t pg[PPT];
 #pragma unroll
   for (int k = 0; k < PPT; ++k) {
@@ -847,6 +855,57 @@ bool dispatch_group(int32_t group, const decode_params &P, dim3 grid, hipStream_
 }
 
 }  // namespace
+
+// Chunked prefill on q8_0 pools, row by row as run_prefill does
+// (text/generator/detail.hpp:4297-4372): row r of sequence s is a decode of
+// q_start[s] + r + 1 tokens through s's block-table row, one split per row,
+// written straight to out (no workspace).  The context of a row must fit
+// one split's page list (k_max_split_pages - 2 pages).
+emel_error_type decode_rows(const pool_layout &L, const void *k_pool, const void *v_pool,
+                            int32_t layer, const float *q, float *out, int32_t n_seq, int32_t n_q,
+                            const int32_t *q_start, const uint16_t *block_tables,
+                            int32_t table_stride, float scale, hipStream_t st) {
+  const int64_t n_rows = static_cast<int64_t>(n_seq) * n_q;
+  if (n_rows > 65535) return EMELK_ERR_INVALID_REQUEST;
+  const int32_t tile = 2 * (k_wave / (L.head_dim / 16));
+  const int64_t bound = static_cast<int64_t>(table_stride) * L.block_tokens;  // longest row context
+  const int64_t max_tps = static_cast<int64_t>(k_max_split_pages - 2) * L.block_tokens / tile * tile;
+  const int64_t tps = (bound + tile - 1) / tile * tile;
+  if (tps > max_tps) return EMELK_ERR_INVALID_REQUEST;
+  decode_params P{};
+  P.L = L;
+  P.k_pool = static_cast<const uint8_t *>(k_pool);
+  P.v_pool = static_cast<const uint8_t *>(v_pool);
+  P.layer = layer;
+  P.q = q;
+  P.kv_lens = nullptr;
+  P.tables = block_tables;
+  P.table_stride = table_stride;
+  P.c = scale * 1.4426950408889634f;
+  P.tokens_per_split = static_cast<int32_t>(tps);
+  P.max_splits = 1;
+  P.part_acc = nullptr;
+  P.part_ml = nullptr;
+  P.new_k = nullptr;
+  P.new_v = nullptr;
+  P.k_wr = nullptr;
+  P.v_wr = nullptr;
+  P.direct_out = out;
+  P.row_q_start = q_start;
+  P.rows = n_q;
+  const dim3 grid(1, L.n_head_kv / waves_per_block(L.n_head_kv), static_cast<uint32_t>(n_rows));
+  const int32_t group = L.n_head / L.n_head_kv;
+  const bool q8 = L.kv_type == EMELK_KV_Q8_0;
+  bool ok;
+  if (L.head_dim == 128) {
+    ok = q8 ? dispatch_group<128, true>(group, P, grid, st) : dispatch_group<128, false>(group, P, grid, st);
+  } else {
+    ok = q8 ? dispatch_group<64, true>(group, P, grid, st) : dispatch_group<64, false>(group, P, grid, st);
+  }
+  if (!ok) return EMELK_ERR_INVALID_REQUEST;
+  return hipGetLastError() == hipSuccess ? EMELK_ERR_NONE : EMELK_ERR_BACKEND;
+}
+
 }  // namespace emelk
 
 extern "C" emel_error_type emelk_attn_decode_workspace_size(const emelk_kv_geometry *g,
@@ -894,6 +953,8 @@ emel_error_type decode_impl(const emelk_kv_geometry *g, const void *k_pool, cons
   P.new_v = new_v;
   // a single split per sequence needs no merge: the decode kernel writes out
   P.direct_out = plan.max_splits == 1 ? out : nullptr;
+  P.row_q_start = nullptr;
+  P.rows = 1;
   P.k_wr = static_cast<uint8_t *>(const_cast<void *>(k_pool));
   P.v_wr = static_cast<uint8_t *>(const_cast<void *>(v_pool));
   const uint64_t acc_floats = static_cast<uint64_t>(n_seq) * L.n_head * plan.max_splits * L.head_dim;

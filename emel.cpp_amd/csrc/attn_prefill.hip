@@ -30,6 +30,7 @@
 
 #include "device_common.hpp"
 #include "emelk.h"
+#include "decode_rows.hpp"
 #include "pool_layout.hpp"
 
 namespace emelk {
@@ -609,12 +610,18 @@ extern "C" emel_error_type emelk_attn_prefill_chunk(const emelk_kv_geometry *g, 
                                                     int32_t table_stride, float scale,
                                                     void *stream) {
   emelk::pool_layout L;
-  if (emelk::make_pool_layout(g, L) != EMELK_ERR_NONE || L.kv_type != EMELK_KV_F16 ||
+  if (emelk::make_pool_layout(g, L) != EMELK_ERR_NONE ||
       k_pool == nullptr || v_pool == nullptr || q == nullptr || out == nullptr ||
       q_start == nullptr || block_tables == nullptr || layer < 0 || layer >= L.n_layer ||
       n_seq <= 0 || n_seq > 65535 || n_q <= 0 || table_stride <= 0 || !(scale > 0.0f) ||
       !std::isfinite(scale)) {
     return EMELK_ERR_INVALID_REQUEST;
+  }
+  if (L.kv_type == EMELK_KV_Q8_0) {
+    // q8_0 pools: row by row through the decode kernel (exact int8 values,
+    // block scales applied in fp32), as the reference's per-row loop does
+    return emelk::decode_rows(L, k_pool, v_pool, layer, q, out, n_seq, n_q, q_start,
+                              block_tables, table_stride, scale, static_cast<hipStream_t>(stream));
   }
   emelk::prefill_params P;
   P.L = L;

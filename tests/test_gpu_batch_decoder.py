@@ -26,12 +26,18 @@ def f16r(x):
     return oracle.fp16_to_fp32(oracle.fp32_to_fp16(np.asarray(x, np.float32)))
 
 
+def q8r(x):
+    x = np.asarray(x, np.float32)
+    return oracle.dequantize_q8_0(oracle.quantize_q8_0(x.reshape(-1, x.shape[-1]))).reshape(x.shape)
+
+
 class Model:
     """Oracle side: per sequence and layer, the stored (roped) K and V rows."""
 
-    def __init__(self):
+    def __init__(self, kv_type=emelk.KV_F16):
         self.k = {}
         self.v = {}
+        self.stored = f16r if kv_type == emelk.KV_F16 else q8r
 
     def ensure(self, seq):
         self.k.setdefault(seq, [[] for _ in range(L)])
@@ -47,16 +53,17 @@ class Model:
         assert len(self.k[seq][layer]) == pos
         self.k[seq][layer].append(ko)
         self.v[seq][layer].append(vo)
-        kk = f16r(np.stack(self.k[seq][layer]))
-        vv = f16r(np.stack(self.v[seq][layer]))
+        kk = self.stored(np.stack(self.k[seq][layer]))
+        vv = self.stored(np.stack(self.v[seq][layer]))
         return oracle.attention_f64(f16r(qo), kk, vv, H, HKV, D, pos + 1, SCALE)
 
 
-def test_batch_decoder_prefill_decode_and_branch(device):
+@pytest.mark.parametrize("kv_type", [emelk.KV_F16, emelk.KV_Q8_0])
+def test_batch_decoder_prefill_decode_and_branch(device, kv_type):
     import torch
-    banner("batch decoder: prefill, decode, branch with device tail split")
+    banner(f"batch decoder: prefill, decode, branch with device tail split, kv_type={kv_type}")
     rng = np.random.default_rng(7)
-    g = emelk.geometry(L, H, HKV, D, BT, 96, emelk.KV_F16)
+    g = emelk.geometry(L, H, HKV, D, BT, 96, kv_type)
     actor = emelk.KvActor()
     assert actor.reserve(8, 96, BT)[0]
     actor.set_free_order(rng.permutation(96).astype(np.uint16))
@@ -69,7 +76,7 @@ def test_batch_decoder_prefill_decode_and_branch(device):
     kn = rng.standard_normal(D).astype(np.float32)
     qn_d = torch.from_numpy(qn).to(device)
     kn_d = torch.from_numpy(kn).to(device)
-    model = Model()
+    model = Model(kv_type)
     for s in range(3):
         model.ensure(s)
 

@@ -640,3 +640,37 @@ def test_decode_at_the_sequence_limit(device):
     assert np.all(got0[7] == 0.0)
     keep = [s for s in range(256) if s != 7]
     np.testing.assert_array_equal(got0[keep], got[keep])
+
+
+def test_prefill_chunk_q8_0_row_by_row(device):
+    """q8_0 pools: the chunk runs row by row through the decode kernel (the
+    reference's per-row route, exact int8 values), checked against the
+    oracle's q8_0 attention for every row."""
+    import torch
+    banner("prefill chunk on q8_0 pools (row by row)")
+    n_head, n_kv, D, bt, n_q = 16, 4, 128, 32, 37
+    q_starts = [0, 100, 1000]
+    lens = [s + n_q for s in q_starts]
+    sc = Scenario(n_layer=1, n_head=n_head, n_kv=n_kv, head_dim=D, block_tokens=bt, lens=lens,
+                  seed=71, kv_type=emelk.KV_Q8_0, outlier_frac=0.01)
+    rng = np.random.default_rng(72)
+    q = rng.standard_normal((sc.n_seq, n_q, n_head, D)).astype(np.float32)
+    qd = torch.from_numpy(q).to(device)
+    out = torch.full_like(qd, float("nan"))
+    qs = torch.tensor(q_starts, dtype=torch.int32, device=device)
+    scale = 1.0 / np.sqrt(D)
+    emelk.prefill_chunk(sc.g, sc.k_pool, sc.v_pool, 0, qd, out, qs, sc.tables, scale)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    kc, vc = sc.oracle_cache(0)
+    for s in range(sc.n_seq):
+        kq = oracle.dequantize_q8_0(oracle.quantize_q8_0(sc.k_rows[0][s]))
+        vq = oracle.dequantize_q8_0(oracle.quantize_q8_0(sc.v_rows[0][s]))
+        for r in range(n_q):
+            limit = q_starts[s] + r + 1  # row r attends causally to [0, q_start + r]
+            want = oracle.compute_attention_q8_0(q[s, r].ravel(), kc, vc, sc.tables_host[s], bt,
+                                                 n_head, n_kv, D, limit, limit, scale)
+            assert_close(got[s, r].ravel(), want, what=f"q8_0 prefill seq {s} row {r}")
+            qr = oracle.fp16_to_fp32(oracle.fp32_to_fp16(q[s, r].ravel()))
+            ideal = oracle.attention_f64(qr, kq[:limit], vq[:limit], n_head, n_kv, D, limit, scale)
+            assert_close(got[s, r].ravel(), ideal, what=f"q8_0 prefill seq {s} row {r} vs ideal")
