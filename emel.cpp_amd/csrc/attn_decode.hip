@@ -854,6 +854,48 @@ bool dispatch_group(int32_t group, const decode_params &P, dim3 grid, hipStream_
   }
 }
 
+template <bool Q8>
+bool dispatch_dim(int32_t head_dim, int32_t group, const decode_params &P, dim3 grid,
+                  hipStream_t st) {
+  switch (head_dim) {
+    case 64: return dispatch_group<64, Q8>(group, P, grid, st);
+    case 128: return dispatch_group<128, Q8>(group, P, grid, st);
+    case 256: return dispatch_group<256, Q8>(group, P, grid, st);
+    case 512: return dispatch_group<512, Q8>(group, P, grid, st);
+    default: return false;
+  }
+}
+
+bool dispatch_decode(const pool_layout &L, const decode_params &P, dim3 grid, hipStream_t st) {
+  const int32_t group = L.n_head / L.n_head_kv;
+  return L.kv_type == EMELK_KV_Q8_0 ? dispatch_dim<true>(L.head_dim, group, P, grid, st)
+                                    : dispatch_dim<false>(L.head_dim, group, P, grid, st);
+}
+
+template <int CH>
+void launch_combine_ch(int32_t head_dim, dim3 grid, hipStream_t st, const decode_params &P,
+                       const int32_t *kv_lens, int32_t n_head, int32_t max_splits, int32_t tps,
+                       float *out) {
+  switch (head_dim) {
+    case 64:
+      hipLaunchKernelGGL((combine_kernel<64, CH>), grid, dim3(64), 0, st, P.part_acc, P.part_ml,
+                         kv_lens, n_head, max_splits, tps, out);
+      break;
+    case 128:
+      hipLaunchKernelGGL((combine_kernel<128, CH>), grid, dim3(128), 0, st, P.part_acc, P.part_ml,
+                         kv_lens, n_head, max_splits, tps, out);
+      break;
+    case 256:
+      hipLaunchKernelGGL((combine_kernel<256, CH>), grid, dim3(256), 0, st, P.part_acc, P.part_ml,
+                         kv_lens, n_head, max_splits, tps, out);
+      break;
+    default:
+      hipLaunchKernelGGL((combine_kernel<512, CH>), grid, dim3(512), 0, st, P.part_acc, P.part_ml,
+                         kv_lens, n_head, max_splits, tps, out);
+      break;
+  }
+}
+
 }  // namespace
 
 // Chunked prefill on q8_0 pools, row by row as run_prefill does
@@ -894,15 +936,7 @@ emel_error_type decode_rows(const pool_layout &L, const void *k_pool, const void
   P.row_q_start = q_start;
   P.rows = n_q;
   const dim3 grid(1, L.n_head_kv / waves_per_block(L.n_head_kv), static_cast<uint32_t>(n_rows));
-  const int32_t group = L.n_head / L.n_head_kv;
-  const bool q8 = L.kv_type == EMELK_KV_Q8_0;
-  bool ok;
-  if (L.head_dim == 128) {
-    ok = q8 ? dispatch_group<128, true>(group, P, grid, st) : dispatch_group<128, false>(group, P, grid, st);
-  } else {
-    ok = q8 ? dispatch_group<64, true>(group, P, grid, st) : dispatch_group<64, false>(group, P, grid, st);
-  }
-  if (!ok) return EMELK_ERR_INVALID_REQUEST;
+  if (!dispatch_decode(L, P, grid, st)) return EMELK_ERR_INVALID_REQUEST;
   return hipGetLastError() == hipSuccess ? EMELK_ERR_NONE : EMELK_ERR_BACKEND;
 }
 
@@ -962,36 +996,15 @@ emel_error_type decode_impl(const emelk_kv_geometry *g, const void *k_pool, cons
   P.part_ml = P.part_acc + acc_floats;
   const dim3 grid(plan.max_splits, L.n_head_kv / emelk::waves_per_block(L.n_head_kv), n_seq);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int32_t group = L.n_head / L.n_head_kv;
-  const bool q8 = L.kv_type == EMELK_KV_Q8_0;
-  bool ok = false;
-  if (L.head_dim == 128) {
-    ok = q8 ? emelk::dispatch_group<128, true>(group, P, grid, st)
-            : emelk::dispatch_group<128, false>(group, P, grid, st);
-  } else {
-    ok = q8 ? emelk::dispatch_group<64, true>(group, P, grid, st)
-            : emelk::dispatch_group<64, false>(group, P, grid, st);
-  }
-  if (!ok) return EMELK_ERR_INVALID_REQUEST;
+  if (!emelk::dispatch_decode(L, P, grid, st)) return EMELK_ERR_INVALID_REQUEST;
   if (P.direct_out != nullptr) return hipGetLastError() == hipSuccess ? EMELK_ERR_NONE : EMELK_ERR_BACKEND;
   const dim3 cgrid(n_seq * L.n_head);
-  const bool wide = plan.max_splits > 16;
-  if (L.head_dim == 128) {
-    if (wide) {
-      hipLaunchKernelGGL((emelk::combine_kernel<128, 64>), cgrid, dim3(128), 0, st, P.part_acc,
-                         P.part_ml, kv_lens, L.n_head, plan.max_splits, plan.tokens_per_split, out);
-    } else {
-      hipLaunchKernelGGL((emelk::combine_kernel<128, 16>), cgrid, dim3(128), 0, st, P.part_acc,
-                         P.part_ml, kv_lens, L.n_head, plan.max_splits, plan.tokens_per_split, out);
-    }
+  if (plan.max_splits > 16) {
+    emelk::launch_combine_ch<64>(L.head_dim, cgrid, st, P, kv_lens, L.n_head, plan.max_splits,
+                                 plan.tokens_per_split, out);
   } else {
-    if (wide) {
-      hipLaunchKernelGGL((emelk::combine_kernel<64, 64>), cgrid, dim3(64), 0, st, P.part_acc,
-                         P.part_ml, kv_lens, L.n_head, plan.max_splits, plan.tokens_per_split, out);
-    } else {
-      hipLaunchKernelGGL((emelk::combine_kernel<64, 16>), cgrid, dim3(64), 0, st, P.part_acc,
-                         P.part_ml, kv_lens, L.n_head, plan.max_splits, plan.tokens_per_split, out);
-    }
+    emelk::launch_combine_ch<16>(L.head_dim, cgrid, st, P, kv_lens, L.n_head, plan.max_splits,
+                                 plan.tokens_per_split, out);
   }
   return hipGetLastError() == hipSuccess ? EMELK_ERR_NONE : EMELK_ERR_BACKEND;
 }

@@ -617,9 +617,11 @@ extern "C" emel_error_type emelk_attn_prefill_chunk(const emelk_kv_geometry *g, 
       !std::isfinite(scale)) {
     return EMELK_ERR_INVALID_REQUEST;
   }
-  if (L.kv_type == EMELK_KV_Q8_0) {
-    // q8_0 pools: row by row through the decode kernel (exact int8 values,
-    // block scales applied in fp32), as the reference's per-row loop does
+  if (L.kv_type == EMELK_KV_Q8_0 || L.head_dim > 128) {
+    // q8_0 pools, and head_dim 256 / 512 (whose O and Q^T tiles do not fit
+    // this kernel's registers): row by row through the decode kernel (exact
+    // int8 values, block scales applied in fp32), as the reference's per-row
+    // loop does
     return emelk::decode_rows(L, k_pool, v_pool, layer, q, out, n_seq, n_q, q_start,
                               block_tables, table_stride, scale, static_cast<hipStream_t>(stream));
   }

@@ -56,15 +56,17 @@ constexpr int k_dpp_quad_xor2 = 0x4E;  // quad_perm [2,3,0,1]
 constexpr int k_dpp_row_half_mirror = 0x141;
 constexpr int k_dpp_row_mirror = 0x140;
 
-// Sum over aligned groups of `lanes` consecutive lanes (lanes in {2,4,8,16});
-// every lane of the group receives the group total.
+// Sum over aligned groups of `lanes` consecutive lanes (lanes in
+// {2,4,8,16,32}); every lane of the group receives the group total.
 template <int lanes>
 __device__ __forceinline__ float group_sum(float v) {
-  static_assert(lanes == 2 || lanes == 4 || lanes == 8 || lanes == 16, "group size");
+  static_assert(lanes == 2 || lanes == 4 || lanes == 8 || lanes == 16 || lanes == 32,
+                "group size");
   v += dpp<k_dpp_quad_xor1>(v);
   if constexpr (lanes >= 4) v += dpp<k_dpp_quad_xor2>(v);
   if constexpr (lanes >= 8) v += dpp<k_dpp_row_half_mirror>(v);
   if constexpr (lanes >= 16) v += dpp<k_dpp_row_mirror>(v);
+  if constexpr (lanes >= 32) v += __shfl_xor(v, 16, 64);  // the neighbouring 16-lane row
   return v;
 }
 

@@ -54,7 +54,7 @@ inline emel_error_type make_pool_layout(const emelk_kv_geometry *g, pool_layout 
   if (g == nullptr) return EMELK_ERR_INVALID_REQUEST;
   const bool type_ok = g->kv_type == EMELK_KV_F16 || g->kv_type == EMELK_KV_Q8_0;
   if (!type_ok || g->n_layer <= 0 || g->n_head <= 0 || g->n_head_kv <= 0 ||
-      g->n_head % g->n_head_kv != 0 || (g->head_dim != 64 && g->head_dim != 128) ||
+      g->n_head % g->n_head_kv != 0 || (g->head_dim != 64 && g->head_dim != 128 && g->head_dim != 256 && g->head_dim != 512) ||
       g->block_tokens <= 0 || g->max_blocks <= 0 || g->max_blocks > EMELK_MAX_BLOCKS) {
     return EMELK_ERR_INVALID_REQUEST;
   }

@@ -44,7 +44,7 @@ namespace {
 using namespace emelk::dev;
 
 constexpr int k_rows_per_wg = 4;
-constexpr int k_max_dim = 128;
+constexpr int k_max_dim = 512;
 
 struct rope_append_args {
   pool_layout L;
@@ -173,15 +173,18 @@ __global__ __launch_bounds__(k_rows_per_wg *k_wave) void rope_append_kernel(rope
   }
   __syncthreads();
 
-  // apply_rope_pairing (detail.hpp:2905-2936): lane p rotates pair p.
-  if (have && kind < 2 && lane < A.pair_count) {
-    const int32_t d0 = lane * A.x0_stride;
-    const int32_t d1 = lane * A.x1_stride + A.x1_base;
-    const float2 cs = A.rope[static_cast<uint64_t>(pos) * A.pair_count + lane];
-    const float x0 = buf[d0];
-    const float x1 = buf[d1];
-    buf[d0] = x0 * cs.x - x1 * cs.y;
-    buf[d1] = x0 * cs.y + x1 * cs.x;
+  // apply_rope_pairing (detail.hpp:2905-2936): lane p rotates pairs p,
+  // p + 64, ... (pairs never overlap, so the order does not matter)
+  if (have && kind < 2) {
+    for (int32_t pr = lane; pr < A.pair_count; pr += k_wave) {
+      const int32_t d0 = pr * A.x0_stride;
+      const int32_t d1 = pr * A.x1_stride + A.x1_base;
+      const float2 cs = A.rope[static_cast<uint64_t>(pos) * A.pair_count + pr];
+      const float x0 = buf[d0];
+      const float x1 = buf[d1];
+      buf[d0] = x0 * cs.x - x1 * cs.y;
+      buf[d1] = x0 * cs.y + x1 * cs.x;
+    }
   }
   __syncthreads();
   if (!have) return;

@@ -200,7 +200,7 @@ typedef struct emelk_kv_geometry {
   int32_t n_layer;
   int32_t n_head;      /* query heads */
   int32_t n_head_kv;   /* key/value heads (GQA: n_head % n_head_kv == 0) */
-  int32_t head_dim;    /* 64 or 128 */
+  int32_t head_dim;    /* 64, 128, 256 or 512 (256 / 512: prefill runs row by row) */
   int32_t block_tokens;/* tokens per page */
   int32_t max_blocks;  /* pages in the pool */
   int32_t kv_type;     /* EMELK_KV_F16 or EMELK_KV_Q8_0 */

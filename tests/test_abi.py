@@ -37,6 +37,7 @@ def test_invalid_geometry_is_rejected():
     out = ctypes.c_uint64(0)
     for bad in [emelk.geometry(1, 6, 4, 128, 16, 8),        # n_head % n_head_kv
                 emelk.geometry(1, 8, 8, 96, 16, 8),         # head_dim
+                emelk.geometry(1, 8, 8, 1024, 16, 8),       # head_dim above 512
                 emelk.geometry(1, 8, 8, 64, 2, 8, emelk.KV_Q8_0),  # q8_0 page too small
                 emelk.geometry(1, 8, 8, 64, 16, 40000),     # max_blocks
                 emelk.geometry(1, 8, 8, 64, 16, 8, 3)]:     # kv_type
@@ -75,7 +76,7 @@ def test_rope_table_rejects_bad_pairings_before_touching_the_gpu():
     assert create(128, (1, 1, 0, 2)) == emelk.ERR_INVALID_REQUEST
     # bad base, head or positions
     assert create(128, emelk.NORMAL_PAIRING, base=0.0) == emelk.ERR_INVALID_REQUEST
-    assert create(128, emelk.NORMAL_PAIRING, head_dim=256) == emelk.ERR_INVALID_REQUEST
+    assert create(128, emelk.NORMAL_PAIRING, head_dim=1024) == emelk.ERR_INVALID_REQUEST
     assert create(128, emelk.NORMAL_PAIRING, max_pos=0) == emelk.ERR_INVALID_REQUEST
     assert not h.value
     # rot_dim <= 1 rotates nothing: a table with no device memory is valid

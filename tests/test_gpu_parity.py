@@ -674,3 +674,59 @@ def test_prefill_chunk_q8_0_row_by_row(device):
             qr = oracle.fp16_to_fp32(oracle.fp32_to_fp16(q[s, r].ravel()))
             ideal = oracle.attention_f64(qr, kq[:limit], vq[:limit], n_head, n_kv, D, limit, scale)
             assert_close(got[s, r].ravel(), ideal, what=f"q8_0 prefill seq {s} row {r} vs ideal")
+
+
+# ---- head_dim 256 and 512 (Gemma-4-sized heads: key_length 512, 256 on
+# sliding-window layers, src/emel/model/gemma4/detail.cpp:26-29) ----
+
+@pytest.mark.parametrize("kv_type,n_head,n_kv,D,bt,lens", [
+    (emelk.KV_F16, 8, 2, 256, 16, [300, 1, 1025]),
+    (emelk.KV_F16, 8, 1, 512, 32, [700, 33]),
+    (emelk.KV_Q8_0, 8, 2, 256, 32, [513, 64]),
+    (emelk.KV_Q8_0, 4, 4, 512, 16, [129, 3000]),
+])
+def test_decode_large_heads(device, kv_type, n_head, n_kv, D, bt, lens):
+    banner(f"decode large heads type={kv_type} H={n_head}/{n_kv} D={D} bt={bt} lens={lens}")
+    sc = Scenario(n_layer=1, n_head=n_head, n_kv=n_kv, head_dim=D, block_tokens=bt, lens=lens,
+                  seed=sum(lens) + D, kv_type=kv_type, outlier_frac=0.01)
+    _decode_case(sc, 0, 800 + D)
+
+
+def test_decode_append_large_heads(device):
+    import torch
+    banner("decode_append at head_dim 256 (f16) and 512 (q8_0)")
+    for kv_type, D in ((emelk.KV_F16, 256), (emelk.KV_Q8_0, 512)):
+        sc = Scenario(n_layer=1, n_head=8, n_kv=2, head_dim=D, block_tokens=16, lens=[47, 200],
+                      seed=D, extra_blocks=4, kv_type=kv_type)
+        for s in range(sc.n_seq):
+            assert sc.actor.allocate_slots(s, 1)[0]
+        sc.refresh_tables()
+        rng = np.random.default_rng(D + 1)
+        nk = rng.standard_normal((sc.n_seq, sc.kv_dim)).astype(np.float32)
+        nv = rng.standard_normal((sc.n_seq, sc.kv_dim)).astype(np.float32)
+        q = rng.standard_normal((sc.n_seq, 8 * D)).astype(np.float32)
+        lens_now = [n + 1 for n in sc.lens]
+        kl = torch.tensor(lens_now, dtype=torch.int32, device=device)
+        ws = torch.zeros(emelk.decode_workspace_bytes(sc.g, sc.n_seq, max(lens_now)) // 4 + 1,
+                         device=device)
+        out = torch.full((sc.n_seq, 8, D), float("nan"), device=device)
+        emelk.decode_append(sc.g, sc.k_pool, sc.v_pool, 0, torch.from_numpy(nk).to(device),
+                            torch.from_numpy(nv).to(device),
+                            torch.from_numpy(q).to(device).view(sc.n_seq, 8, D), out, kl,
+                            max(lens_now), sc.tables, float(1 / np.sqrt(D)), ws)
+        torch.cuda.synchronize()
+        for s in range(sc.n_seq):
+            sc.k_rows[0][s] = np.concatenate([sc.k_rows[0][s], nk[s][None]])
+            sc.v_rows[0][s] = np.concatenate([sc.v_rows[0][s], nv[s][None]])
+        sc.lens = lens_now
+        assert_close(out.view(sc.n_seq, -1).cpu().numpy(), sc.oracle_decode(0, q),
+                     what=f"decode_append D={D}")
+        for which, pool in (("k", sc.k_pool), ("v", sc.v_pool)):
+            np.testing.assert_array_equal(pool.cpu().numpy(), sc.expected_pool(which),
+                                          err_msg=f"{which} pool D={D}")
+
+
+def test_prefill_chunk_large_heads(device):
+    # head_dim 256 takes the row-by-row route through the decode kernel
+    banner("prefill chunk at head_dim 256 (row by row)")
+    _prefill_case(device, 8, 2, 256, 16, [0, 130], 21, seed=81)

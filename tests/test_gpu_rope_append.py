@@ -136,3 +136,15 @@ def test_qkv_rope_append_skips_tokens_outside_table_and_pool(device):
     torch.cuda.synchronize()
     assert np.all(q_out.cpu().numpy()[0, 0] == 7.0)
     rope.close()
+
+
+@pytest.mark.parametrize("kv_type,D,n_rot,pairing", [
+    (emelk.KV_F16, 256, 256, emelk.NEOX_PAIRING),
+    (emelk.KV_Q8_0, 512, 512, emelk.NORMAL_PAIRING),
+    (emelk.KV_F16, 512, 128, emelk.NEOX_PAIRING),     # partial rotation
+])
+def test_qkv_rope_append_large_heads_bit_exact(device, kv_type, D, n_rot, pairing):
+    """head_dim 256 and 512 (more rotation pairs than lanes): q and pool
+    bytes bit-exact, with both norms."""
+    case = (kv_type, 8, 2, D, 16, pairing, n_rot, 1e6, True, True, [21, 5])
+    test_qkv_rope_append_is_bit_exact(device, case)
