@@ -61,6 +61,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="llama3-8b-b64-ctx8k",
                     choices=sorted(CONFIGS) + ["llama3-8b-prefill512-evict25",
+                                               "llama3-8b-q8_0-prefill512-evict25",
                                                "llama3-8b-b64-ctx8k-generator"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--separate-append", action="store_true",
@@ -92,7 +93,7 @@ def main():
         return
     import emelk
 
-    if args.config == "llama3-8b-prefill512-evict25":
+    if args.config in ("llama3-8b-prefill512-evict25", "llama3-8b-q8_0-prefill512-evict25"):
         return prefill_evict(args, torch, emelk, dev)
     if args.config == "llama3-8b-b64-ctx8k-generator":
         return generator(args, torch, emelk, dev)
@@ -322,8 +323,12 @@ def prefill_evict(args, torch, emelk, dev):
     """8 sequences with 4096 cached tokens each
     append a 512-token chunk (per layer: chunk append + causal chunk attention
     on MFMA, f16 in, fp32 accumulate), then 25% of each sequence's pages are
-    evicted and the survivors compacted by a generated move list."""
+    evicted and the survivors compacted by a generated move list.  The
+    q8_0 variant runs the same workload on q8_0 pools (the prefix is stored
+    through the quantizing append; K/V are dequantized to fp16 while staged
+    for the MFMAs)."""
     L, H, HK, D, BT, B, P0, NQ = 32, 32, 8, 128, 32, 8, 4096, 512
+    q8 = "q8_0" in args.config
     rng = np.random.default_rng(args.seed)
     total = P0 + NQ
     pages = -(-total // BT)
@@ -338,14 +343,28 @@ def prefill_evict(args, torch, emelk, dev):
         assert actor.allocate_slots(s, NQ)[0]  # the chunk's slots
     stride = pages + 1
     tables = torch.from_numpy(actor.export_block_tables(list(range(B)), stride).view(np.int16)).to(dev)
-    g = emelk.geometry(L, H, HK, D, BT, max_blocks)
+    g = emelk.geometry(L, H, HK, D, BT, max_blocks, emelk.KV_Q8_0 if q8 else emelk.KV_F16)
     pb = emelk.pool_bytes(g)
+    page_bytes = pb // (L * max_blocks)
     k_pool = torch.empty(pb, dtype=torch.uint8, device=dev)
     v_pool = torch.empty(pb, dtype=torch.uint8, device=dev)
     gen = torch.Generator(device=dev)
     gen.manual_seed(args.seed)
-    k_pool.view(torch.float16).normal_(generator=gen)
-    v_pool.view(torch.float16).normal_(generator=gen)
+    if q8:
+        # the prefix through the quantizing append (1% outliers x20, as config 4)
+        zero = torch.zeros((B,), dtype=torch.int32, device=dev)
+        for layer in range(L):
+            rows = []
+            for _ in range(2):
+                x = torch.randn((B, P0, HK * D), generator=gen, device=dev)
+                x = torch.where(torch.rand(x.shape, generator=gen, device=dev) < 0.01, x * 20.0, x)
+                rows.append(x)
+            emelk.append(g, k_pool, v_pool, layer, rows[0], rows[1], zero, tables)
+            del rows
+        torch.cuda.synchronize()
+    else:
+        k_pool.view(torch.float16).normal_(generator=gen)
+        v_pool.view(torch.float16).normal_(generator=gen)
     q = [torch.randn((B, NQ, H, D), generator=gen, device=dev) for _ in range(L)]
     ck = [torch.randn((B, NQ, HK * D), generator=gen, device=dev) for _ in range(L)]
     cv = [torch.randn((B, NQ, HK * D), generator=gen, device=dev) for _ in range(L)]
@@ -396,13 +415,14 @@ def prefill_evict(args, torch, emelk, dev):
     e1.record(stream)
     torch.cuda.synchronize()
     copy_ms = e0.elapsed_time(e1)
-    copy_bytes = 2 * 2 * len(moves) * L * (HK * BT * D * 2)  # read + write, K and V
+    copy_bytes = 2 * 2 * len(moves) * L * page_bytes  # read + write, K and V
     res = {
         "metric": "chunked-prefill attention TFLOP/s (MFMA f16, fp32 acc) + compaction GB/s",
+        "kv_type": "q8_0" if q8 else "f16",
         "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": K,
         "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True,
         "dtype": "f16", "data": "synthetic (seeded N(0,1), seeded page permutation)",
-        "config": {"workload": "llama3-8b-prefill512-evict25", "batch": B, "prefix": P0,
+        "config": {"workload": args.config, "batch": B, "prefix": P0,
                    "chunk": NQ, "n_layer": L, "block_tokens": BT},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": 2500.0,
                      "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4), "traffic": None,

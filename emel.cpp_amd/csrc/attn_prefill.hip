@@ -44,6 +44,7 @@ constexpr int k_max_seq_pages = EMELK_MAX_BLOCKS_PER_SEQUENCE;  // LDS page list
 
 typedef _Float16 half8_v __attribute__((ext_vector_type(8)));
 typedef float float16_v __attribute__((ext_vector_type(16)));
+typedef uint32_t uint2_v __attribute__((ext_vector_type(2)));
 
 struct prefill_params {
   pool_layout L;
@@ -60,6 +61,39 @@ struct prefill_params {
   int32_t bt_shift;  // log2(block_tokens) when a power of two, else -1
 };
 
+// Register staging of one key tile.  f16 pools: K as 16-byte row chunks, V
+// as 4 keys x 2 dims.  q8_0 pools: the same items at one byte per value plus
+// each value block's fp16 scale (V words hold the int8 pair in the low and
+// the scale in the high 16 bits); they become fp16 when written to LDS.
+template <int KI, int VI, bool Q8>
+struct prefill_stage {
+  uint4_t rk[KI];
+  uint32_t rv[VI][4];
+};
+template <int KI, int VI>
+struct prefill_stage<KI, VI, true> {
+  uint2_v rk[KI];
+  uint32_t ks[KI];
+  uint32_t rv[VI][4];
+};
+
+// q8_0 -> two fp16 planes for LDS whose sum is exactly q * d, so the MFMAs
+// see the dequantized values of dequantize_row_q8_0 (kernel/detail.hpp:
+// 679-690) without rounding: q is exact in fp16 (a byte under the exponent
+// of 1024, biased by 1152); hi = fp16(q * d) and lo = fma(q, d, -hi), which
+// is exact: q * d has at most 7 + 11 significant bits, hi holds the top 11,
+// and the remainder is a multiple of d's ulp (>= 2^-24, an fp16 subnormal
+// step) below 2^7 of them.  Two values per packed op.  Only |q * d| at or
+// beyond 65520 (outside fp16) does not hold, since hi is then infinite.
+// Returns (hi, lo).
+__device__ __forceinline__ uint2_v q8_pair_to_f16x2(uint32_t bytes2, half2_t d2) {
+  const uint32_t u = bytes2 ^ 0x8080u;
+  const half2_t q = as_half2(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) -
+                    half2_t{1152, 1152};
+  const half2_t h = q * d2;
+  return uint2_v{as_u32(h), as_u32(__builtin_elementwise_fma(q, d2, -h))};
+}
+
 // Slot of key k (0..31) in the MFMA k-order of the score accumulator:
 // accumulator register r of lane-half h holds key 8*(r/4) + 4*h + r%4; the
 // P operand of k-step s uses registers 8s..8s+7, i.e. slot s*16 + 8*h + i
@@ -72,7 +106,7 @@ __device__ __forceinline__ int key_slot(int k) {
   return s * 16 + h * 8 + i;
 }
 
-template <int D, int G_WG, int RB, int KT>
+template <int D, int G_WG, int RB, int KT, bool Q8>
 __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_params P) {
   constexpr int WAVES = G_WG * RB;
   constexpr int NT = WAVES * k_wave;
@@ -86,10 +120,14 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
   constexpr int VITEMS = (KT / 4) * (D / 2);
   constexpr int KI = (KITEMS + NT - 1) / NT;
   constexpr int VI = (VITEMS + NT - 1) / NT;
+  constexpr uint32_t ROWB = Q8 ? D : 2 * D;  // bytes of one K/V row in a page
+  constexpr uint32_t SROWB = D / 16;         // q8_0: bytes of one row's scales
 
-  __shared__ half_t s_k[2][KT][KROW];
+  // q8_0: a hi and a lo plane of K and of V^T (their sum is exact)
+  constexpr int PL = Q8 ? 2 : 1;
+  __shared__ half_t s_k[2][PL][KT][KROW];
   constexpr int VR = 2;  // V double buffer
-  __shared__ half_t s_vt[VR][D][VROW];
+  __shared__ half_t s_vt[VR][PL][D][VROW];
   __shared__ float s_row[WAVES][32];
   __shared__ uint16_t s_ptab[k_max_seq_pages];
 
@@ -180,23 +218,26 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
   // 4 consecutive keys x 2 dims (dims fastest keeps each key row coalesced),
   // transposed in registers so each dim's 4 keys reach LDS as one 8-byte
   // store in the accumulator's key order.
-  struct stage_t {
-    uint4_t rk[KI];
-    uint32_t rv[VI][4];
-  };
+  using stage_t = prefill_stage<KI, VI, Q8>;
+  const uint32_t splane = static_cast<uint32_t>(P.L.block_tokens) * D;  // q8_0 scale plane
 
   // Page of a key from the LDS copy of this sequence's page list (no
   // dependent global load between a tile's address and its data).
   const int bt = P.L.block_tokens;
   const int bt_shift = P.bt_shift;  // log2(block_tokens), or -1
-  auto key_offset = [&](int key, uint32_t &ok) -> uint64_t {
+  // Returns the key's region base (its page, this KV head) and its row.
+  auto key_region = [&](int key, uint32_t &ok, uint32_t &row) -> uint64_t {
     const int lb = bt_shift >= 0 ? key >> bt_shift : key / bt;
-    const int row = bt_shift >= 0 ? key & (bt - 1) : key % bt;
+    row = static_cast<uint32_t>(bt_shift >= 0 ? key & (bt - 1) : key % bt);
     // a sequence holds at most k_max_seq_pages pages (MAX_BLOCKS_PER_SEQUENCE)
     const uint32_t page = (key < total && lb < n_pt) ? s_ptab[lb] : 0xFFFFu;
     ok = page != 0xFFFFu ? 1u : 0u;
-    return layer_base + static_cast<uint64_t>(ok ? page : 0u) * P.L.page_bytes +
-           static_cast<uint64_t>(row) * D * 2u;
+    return layer_base + static_cast<uint64_t>(ok ? page : 0u) * P.L.page_bytes;
+  };
+  // f16: byte offset of the key's row.
+  auto key_offset = [&](int key, uint32_t &ok) -> uint64_t {
+    uint32_t row;
+    return key_region(key, ok, row) + static_cast<uint64_t>(row) * D * 2u;
   };
   // Uniform sub-tiles (block_tokens a multiple of 32): each 32-key sub-tile
   // lies in one page, so its base address is wave-uniform and every thread
@@ -204,25 +245,31 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
   // get zero V (their P is 0, and 0 * garbage could be NaN); a sub-tile on an
   // invalid page is all zeros, as the general path gives.
   const bool uniform_tiles = bt_shift >= 5;
-  uint32_t kofs[KI], vofs[VI];
+  // Offsets inside a 32-key sub-tile (q8_0: of the values, and of the
+  // scale of the item's 32-value block from the scale plane).
+  uint32_t kofs[KI], vofs[VI], ksofs[KI], vsofs[VI];
   int ksub[KI], vsub[VI];
 #pragma unroll
   for (int i = 0; i < KI; ++i) {
     const int item = tid + i * NT;
     const int key = item / (D / 8);
+    const int chunk = item % (D / 8);
     ksub[i] = key / k_sub;
-    kofs[i] = static_cast<uint32_t>((key % k_sub) * D * 2 + (item % (D / 8)) * 16);
+    kofs[i] = static_cast<uint32_t>(key % k_sub) * ROWB + chunk * (ROWB / (D / 8));
+    ksofs[i] = static_cast<uint32_t>(key % k_sub) * SROWB + (chunk / 4) * 2;
   }
 #pragma unroll
   for (int i = 0; i < VI; ++i) {
     const int item = tid + i * NT;
     const int key = 4 * (item / (D / 2));
+    const int dp = item % (D / 2);
     vsub[i] = key / k_sub;
-    vofs[i] = static_cast<uint32_t>((key % k_sub) * D * 2 + 4 * (item % (D / 2)));
+    vofs[i] = static_cast<uint32_t>(key % k_sub) * ROWB + dp * (ROWB / (D / 2));
+    vsofs[i] = static_cast<uint32_t>(key % k_sub) * SROWB + (dp / 16) * 2;
   }
-  auto load_tile_uniform = [&](int t, stage_t &R) {
+  auto load_tile_uniform = [&](int t, stage_t &R) __attribute__((always_inline)) {
     const int key0 = t * KT;
-    uint64_t base[NS];
+    uint64_t base[NS], sbase[NS];  // values, and (q8_0) scales, of each sub-tile's first key
     bool valid[NS];
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
@@ -231,8 +278,9 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
       const uint32_t page = __builtin_amdgcn_readfirstlane(
           (kj < total && lb < n_pt) ? static_cast<uint32_t>(s_ptab[lb]) : 0xFFFFu);
       valid[j] = page != 0xFFFFu;
-      base[j] = layer_base + static_cast<uint64_t>(valid[j] ? page : 0u) * P.L.page_bytes +
-                static_cast<uint64_t>(kj & (bt - 1)) * D * 2u;
+      const uint64_t reg = layer_base + static_cast<uint64_t>(valid[j] ? page : 0u) * P.L.page_bytes;
+      base[j] = reg + static_cast<uint64_t>(kj & (bt - 1)) * ROWB;
+      if constexpr (Q8) sbase[j] = reg + splane + static_cast<uint64_t>(kj & (bt - 1)) * SROWB;
     }
     // Loads are unconditional; the fix-ups below sit behind one uniform
     // branch, so the common path never waits for the data here (a select
@@ -240,16 +288,30 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
 #pragma unroll
     for (int i = 0; i < KI; ++i) {
       if (KITEMS % NT == 0 || tid + i * NT < KITEMS) {
-        R.rk[i] = load16(P.k_pool + base[NS == 1 ? 0 : ksub[i]] + kofs[i]);
+        const int j = NS == 1 ? 0 : ksub[i];
+        if constexpr (Q8) {
+          R.rk[i] = *reinterpret_cast<const uint2_v *>(P.k_pool + (base[j] + kofs[i]));
+          R.ks[i] = *reinterpret_cast<const uint16_t *>(P.k_pool + (sbase[j] + ksofs[i]));
+        } else {
+          R.rk[i] = load16(P.k_pool + (base[j] + kofs[i]));
+        }
       }
     }
 #pragma unroll
     for (int i = 0; i < VI; ++i) {
       if (VITEMS % NT == 0 || tid + i * NT < VITEMS) {
-        const uint64_t vb = base[NS == 1 ? 0 : vsub[i]] + vofs[i];
+        const int j = NS == 1 ? 0 : vsub[i];
+        const uint64_t vb = base[j] + vofs[i];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          R.rv[i][e] = *reinterpret_cast<const uint32_t *>(P.v_pool + vb + e * D * 2);
+          if constexpr (Q8) {
+            const uint64_t sb = sbase[j] + vsofs[i];
+            const uint32_t q = *reinterpret_cast<const uint16_t *>(P.v_pool + vb + e * ROWB);
+            const uint32_t d = *reinterpret_cast<const uint16_t *>(P.v_pool + sb + e * SROWB);
+            R.rv[i][e] = q | (d << 16);
+          } else {
+            R.rv[i][e] = *reinterpret_cast<const uint32_t *>(P.v_pool + vb + e * ROWB);
+          }
         }
       }
     }
@@ -259,7 +321,14 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
     if (!all_valid || key0 + KT > total) {
 #pragma unroll
       for (int i = 0; i < KI; ++i) {
-        if (!valid[NS == 1 ? 0 : ksub[i]]) R.rk[i] = uint4_t{0u, 0u, 0u, 0u};
+        if (!valid[NS == 1 ? 0 : ksub[i]]) {
+          if constexpr (Q8) {
+            R.rk[i] = uint2_v{0u, 0u};
+            R.ks[i] = 0u;
+          } else {
+            R.rk[i] = uint4_t{0u, 0u, 0u, 0u};
+          }
+        }
       }
 #pragma unroll
       for (int i = 0; i < VI; ++i) {
@@ -270,50 +339,104 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
       }
     }
   };
-  auto load_tile_general = [&](int t, stage_t &R) {
+  auto load_tile_general = [&](int t, stage_t &R) __attribute__((always_inline)) {
+    if constexpr (Q8) {
 #pragma unroll
-    for (int i = 0; i < KI; ++i) {
-      const int item = tid + i * NT;
-      if (KITEMS % NT == 0 || item < KITEMS) {
-        uint32_t ok;
-        const uint64_t off = key_offset(t * KT + item / (D / 8), ok) + (item % (D / 8)) * 16u;
-        R.rk[i] = ok ? load16(P.k_pool + off) : uint4_t{0u, 0u, 0u, 0u};
+      for (int i = 0; i < KI; ++i) {
+        const int item = tid + i * NT;
+        if (KITEMS % NT == 0 || item < KITEMS) {
+          uint32_t ok, row;
+          const uint64_t reg = key_region(t * KT + item / (D / 8), ok, row);
+          const uint32_t chunk = item % (D / 8);
+          R.rk[i] = ok ? *reinterpret_cast<const uint2_v *>(P.k_pool + reg + row * ROWB + chunk * 8u)
+                       : uint2_v{0u, 0u};
+          R.ks[i] = ok ? *reinterpret_cast<const uint16_t *>(P.k_pool + reg + splane + row * SROWB +
+                                                             (chunk / 4) * 2u)
+                       : 0u;
+        }
       }
-    }
 #pragma unroll
-    for (int i = 0; i < VI; ++i) {
-      const int item = tid + i * NT;
-      if (VITEMS % NT == 0 || item < VITEMS) {
-        const int dp = item % (D / 2);
-        const int key0 = t * KT + 4 * (item / (D / 2));
-        // the 4 keys share a page whenever block_tokens is a multiple of 4
-        const bool same_page = (bt & 3) == 0;
-        uint32_t ok0;
-        const uint64_t off0 = key_offset(key0, ok0) + 4u * dp;
+      for (int i = 0; i < VI; ++i) {
+        const int item = tid + i * NT;
+        if (VITEMS % NT == 0 || item < VITEMS) {
+          const int dp = item % (D / 2);
+          const int key0 = t * KT + 4 * (item / (D / 2));
+          // the 4 keys share a page whenever block_tokens is a multiple of 4
+          const bool same_page = (bt & 3) == 0;
+          uint32_t ok0, row0;
+          const uint64_t reg0 = key_region(key0, ok0, row0);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          uint32_t ok = ok0;
-          uint64_t off = off0 + static_cast<uint64_t>(j) * D * 2u;
-          if (!same_page) off = key_offset(key0 + j, ok) + 4u * dp;
-          ok = ok && (key0 + j < total);
-          R.rv[i][j] = ok ? *reinterpret_cast<const uint32_t *>(P.v_pool + off) : 0u;
+          for (int j = 0; j < 4; ++j) {
+            uint32_t ok = ok0, row = row0 + j;
+            uint64_t reg = reg0;
+            if (!same_page) reg = key_region(key0 + j, ok, row);
+            ok = ok && (key0 + j < total);
+            const uint32_t q =
+                ok ? *reinterpret_cast<const uint16_t *>(P.v_pool + reg + row * ROWB + 2u * dp) : 0u;
+            const uint32_t d = ok ? *reinterpret_cast<const uint16_t *>(
+                                        P.v_pool + reg + splane + row * SROWB + (dp / 16) * 2u)
+                                  : 0u;
+            R.rv[i][j] = q | (d << 16);
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < KI; ++i) {
+        const int item = tid + i * NT;
+        if (KITEMS % NT == 0 || item < KITEMS) {
+          uint32_t ok;
+          const uint64_t off = key_offset(t * KT + item / (D / 8), ok) + (item % (D / 8)) * 16u;
+          R.rk[i] = ok ? load16(P.k_pool + off) : uint4_t{0u, 0u, 0u, 0u};
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < VI; ++i) {
+        const int item = tid + i * NT;
+        if (VITEMS % NT == 0 || item < VITEMS) {
+          const int dp = item % (D / 2);
+          const int key0 = t * KT + 4 * (item / (D / 2));
+          // the 4 keys share a page whenever block_tokens is a multiple of 4
+          const bool same_page = (bt & 3) == 0;
+          uint32_t ok0;
+          const uint64_t off0 = key_offset(key0, ok0) + 4u * dp;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            uint32_t ok = ok0;
+            uint64_t off = off0 + static_cast<uint64_t>(j) * D * 2u;
+            if (!same_page) off = key_offset(key0 + j, ok) + 4u * dp;
+            ok = ok && (key0 + j < total);
+            R.rv[i][j] = ok ? *reinterpret_cast<const uint32_t *>(P.v_pool + off) : 0u;
+          }
         }
       }
     }
   };
-  auto load_tile = [&](int t, stage_t &R) {
+  auto load_tile = [&](int t, stage_t &R) __attribute__((always_inline)) {
     if (uniform_tiles) {
       load_tile_uniform(t, R);
     } else {
       load_tile_general(t, R);
     }
   };
-  auto store_tile = [&](int kbuf, int vbuf, const stage_t &R) {
+  auto store_tile = [&](int kbuf, int vbuf, const stage_t &R) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < KI; ++i) {
       const int item = tid + i * NT;
       if (KITEMS % NT == 0 || item < KITEMS) {
-        *reinterpret_cast<uint4_t *>(&s_k[kbuf][item / (D / 8)][(item % (D / 8)) * 8]) = R.rk[i];
+        const int krow = item / (D / 8);
+        const int kcol = (item % (D / 8)) * 8;
+        if constexpr (Q8) {
+          const half2_t d2 = as_half2(R.ks[i] * 0x10001u);
+          const uint2_v a = q8_pair_to_f16x2(R.rk[i].x & 0xFFFFu, d2);
+          const uint2_v b = q8_pair_to_f16x2(R.rk[i].x >> 16, d2);
+          const uint2_v c = q8_pair_to_f16x2(R.rk[i].y & 0xFFFFu, d2);
+          const uint2_v e = q8_pair_to_f16x2(R.rk[i].y >> 16, d2);
+          *reinterpret_cast<uint4_t *>(&s_k[kbuf][0][krow][kcol]) = uint4_t{a.x, b.x, c.x, e.x};
+          *reinterpret_cast<uint4_t *>(&s_k[kbuf][PL - 1][krow][kcol]) = uint4_t{a.y, b.y, c.y, e.y};
+        } else {
+          *reinterpret_cast<uint4_t *>(&s_k[kbuf][0][krow][kcol]) = R.rk[i];
+        }
       }
     }
 #pragma unroll
@@ -323,21 +446,33 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
         const int dp = item % (D / 2);
         const int key4 = 4 * (item / (D / 2));  // 4 consecutive keys -> 4 slots
         const int slot = (key4 / k_sub) * k_sub + key_slot(key4 % k_sub);
-        const uint32_t *w = R.rv[i];
-        const uint32_t lo01 = __builtin_amdgcn_perm(w[1], w[0], 0x05040100u);
-        const uint32_t lo23 = __builtin_amdgcn_perm(w[3], w[2], 0x05040100u);
-        const uint32_t hi01 = __builtin_amdgcn_perm(w[1], w[0], 0x07060302u);
-        const uint32_t hi23 = __builtin_amdgcn_perm(w[3], w[2], 0x07060302u);
         // lanes 8..15 of each 16 write their odd row first: the two rows of
         // a lane are 4 banks apart, so each write instruction spreads over
         // twice as many banks (measured: LDS bank-conflict cycles 13.5M ->
         // 4.5M per launch at the Llama-3-8B chunk shape)
         const bool odd_first = (tid & 8) != 0;
         const int r0 = 2 * dp + (odd_first ? 1 : 0);
-        const uint2 first = odd_first ? uint2{hi01, hi23} : uint2{lo01, lo23};
-        const uint2 second = odd_first ? uint2{lo01, lo23} : uint2{hi01, hi23};
-        *reinterpret_cast<uint2 *>(&s_vt[vbuf][r0][slot]) = first;
-        *reinterpret_cast<uint2 *>(&s_vt[vbuf][r0 ^ 1][slot]) = second;
+        auto put = [&](uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3, int plane) {
+          const uint32_t lo01 = __builtin_amdgcn_perm(w1, w0, 0x05040100u);
+          const uint32_t lo23 = __builtin_amdgcn_perm(w3, w2, 0x05040100u);
+          const uint32_t hi01 = __builtin_amdgcn_perm(w1, w0, 0x07060302u);
+          const uint32_t hi23 = __builtin_amdgcn_perm(w3, w2, 0x07060302u);
+          const uint2 first = odd_first ? uint2{hi01, hi23} : uint2{lo01, lo23};
+          const uint2 second = odd_first ? uint2{lo01, lo23} : uint2{hi01, hi23};
+          *reinterpret_cast<uint2 *>(&s_vt[vbuf][plane][r0][slot]) = first;
+          *reinterpret_cast<uint2 *>(&s_vt[vbuf][plane][r0 ^ 1][slot]) = second;
+        };
+        if constexpr (Q8) {
+          uint2_v w[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            w[e] = q8_pair_to_f16x2(R.rv[i][e] & 0xFFFFu, as_half2((R.rv[i][e] >> 16) * 0x10001u));
+          }
+          put(w[0].x, w[1].x, w[2].x, w[3].x, 0);
+          put(w[0].y, w[1].y, w[2].y, w[3].y, PL - 1);
+        } else {
+          put(R.rv[i][0], R.rv[i][1], R.rv[i][2], R.rv[i][3], 0);
+        }
       }
     }
   };
@@ -355,17 +490,20 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
 #pragma unroll
     for (int kk = 0; kk < KSTEPS; ++kk) {
 #pragma unroll
-      for (int j = 0; j < NS; ++j) {
-        const half8_v a =
-            *reinterpret_cast<const half8_v *>(&s_k[buf][j * k_sub + l32][16 * kk + 8 * h]);
-        s[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qop[kk], s[j], 0, 0, 0);
+      for (int pl = 0; pl < PL; ++pl) {
+#pragma unroll
+        for (int j = 0; j < NS; ++j) {
+          const half8_v a = *reinterpret_cast<const half8_v *>(
+              &s_k[buf][pl][j * k_sub + l32][16 * kk + 8 * h]);
+          s[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qop[kk], s[j], 0, 0, 0);
+        }
       }
     }
     if constexpr (NS > 1) {
       // operand reads just ahead of their MFMAs rather than all hoisted,
-      // which would need 4 * NS * KSTEPS registers at once
+      // which would need 4 * NS * KSTEPS * PL registers at once
 #pragma unroll
-      for (int kk = 0; kk < KSTEPS; ++kk) {
+      for (int kk = 0; kk < KSTEPS * PL; ++kk) {
         __builtin_amdgcn_sched_group_barrier(0x100, NS, 0);
         __builtin_amdgcn_sched_group_barrier(0x008, NS, 0);
       }
@@ -494,9 +632,12 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
         for (int i = 0; i < 8; ++i) pa[i] = static_cast<half_t>(s[j][8 * st + i]);
 #pragma unroll
         for (int c = 0; c < DCH; ++c) {
-          const half8_v b = *reinterpret_cast<const half8_v *>(
-              &s_vt[buf][32 * c + l32][j * k_sub + 16 * st + 8 * h]);
-          o[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, b, o[c], 0, 0, 0);
+#pragma unroll
+          for (int pl = 0; pl < PL; ++pl) {
+            const half8_v b = *reinterpret_cast<const half8_v *>(
+                &s_vt[buf][pl][32 * c + l32][j * k_sub + 16 * st + 8 * h]);
+            o[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, b, o[c], 0, 0, 0);
+          }
         }
       }
     }
@@ -570,7 +711,7 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
   }
 }
 
-template <int D, int KT>
+template <int D, int KT, bool Q8>
 bool launch_prefill_kt(const prefill_params &P, int32_t n_seq, hipStream_t st) {
   // 8 waves per workgroup: G_WG query heads of one KV group x RB blocks of
   // 32 query rows, all sharing each staged K/V tile.
@@ -581,10 +722,10 @@ bool launch_prefill_kt(const prefill_params &P, int32_t n_seq, hipStream_t st) {
   const dim3 grid(n_qt * (P.L.n_head / g_wg) * n_seq);
   const dim3 block(8 * k_wave);
   switch (g_wg) {
-    case 1: hipLaunchKernelGGL((prefill_kernel<D, 1, 8, KT>), grid, block, 0, st, P); return true;
-    case 2: hipLaunchKernelGGL((prefill_kernel<D, 2, 4, KT>), grid, block, 0, st, P); return true;
-    case 4: hipLaunchKernelGGL((prefill_kernel<D, 4, 2, KT>), grid, block, 0, st, P); return true;
-    case 8: hipLaunchKernelGGL((prefill_kernel<D, 8, 1, KT>), grid, block, 0, st, P); return true;
+    case 1: hipLaunchKernelGGL((prefill_kernel<D, 1, 8, KT, Q8>), grid, block, 0, st, P); return true;
+    case 2: hipLaunchKernelGGL((prefill_kernel<D, 2, 4, KT, Q8>), grid, block, 0, st, P); return true;
+    case 4: hipLaunchKernelGGL((prefill_kernel<D, 4, 2, KT, Q8>), grid, block, 0, st, P); return true;
+    case 8: hipLaunchKernelGGL((prefill_kernel<D, 8, 1, KT, Q8>), grid, block, 0, st, P); return true;
     default: return false;
   }
 }
@@ -596,7 +737,8 @@ constexpr int k_key_tile = 64;
 
 template <int D>
 bool launch_prefill(const prefill_params &P, int32_t n_seq, hipStream_t st) {
-  return launch_prefill_kt<D, k_key_tile>(P, n_seq, st);
+  if (P.L.kv_type == EMELK_KV_Q8_0) return launch_prefill_kt<D, k_key_tile, true>(P, n_seq, st);
+  return launch_prefill_kt<D, k_key_tile, false>(P, n_seq, st);
 }
 
 }  // namespace
@@ -617,11 +759,10 @@ extern "C" emel_error_type emelk_attn_prefill_chunk(const emelk_kv_geometry *g, 
       !std::isfinite(scale)) {
     return EMELK_ERR_INVALID_REQUEST;
   }
-  if (L.kv_type == EMELK_KV_Q8_0 || L.head_dim > 128) {
-    // q8_0 pools, and head_dim 256 / 512 (whose O and Q^T tiles do not fit
-    // this kernel's registers): row by row through the decode kernel (exact
-    // int8 values, block scales applied in fp32), as the reference's per-row
-    // loop does
+  if (L.head_dim > 128) {
+    // head_dim 256 / 512 (whose O and Q^T tiles do not fit this kernel's
+    // registers): row by row through the decode kernel, as the reference's
+    // per-row loop does
     return emelk::decode_rows(L, k_pool, v_pool, layer, q, out, n_seq, n_q, q_start,
                               block_tables, table_stride, scale, static_cast<hipStream_t>(stream));
   }

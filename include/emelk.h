@@ -278,10 +278,12 @@ emel_error_type emelk_attn_decode_append(const emelk_kv_geometry *g, void *k_poo
  * [n_seq][n_q][n_head][head_dim]; row r of sequence s attends causally to
  * logical positions [0, q_start[s] + r] (the chunk must already be appended).
  * Replaces the per-row store + attend loop of run_prefill
- * (text/generator/detail.hpp:4297-4372).  f16 pools run on MFMA; q8_0 pools
- * run row by row through the decode kernel (n_seq * n_q <= 65535, and a
- * row's context, table_stride * block_tokens tokens at most, must fit 1022
- * pages). */
+ * (text/generator/detail.hpp:4297-4372).  head_dim 64 and 128 run on MFMA,
+ * f16 and q8_0 pools alike (q8_0 values enter the MFMAs exactly, as two
+ * fp16 parts; values of magnitude 65520 or more do not fit).  head_dim 256
+ * and 512 run row by row through the decode kernel (n_seq * n_q <= 65535,
+ * and a row's context, table_stride * block_tokens tokens at most, must fit
+ * 1022 pages). */
 emel_error_type emelk_attn_prefill_chunk(const emelk_kv_geometry *g, const void *k_pool,
                                          const void *v_pool, int32_t layer, const float *q,
                                          float *out, int32_t n_seq, int32_t n_q,
