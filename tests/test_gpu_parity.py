@@ -139,6 +139,43 @@ def test_copy_blocks_and_compaction_are_bit_exact(device):
                 np.testing.assert_array_equal(got, want)
 
 
+@pytest.mark.parametrize("kv_type,D,bt", [(emelk.KV_F16, 128, 32), (emelk.KV_Q8_0, 128, 32),
+                                          (emelk.KV_Q8_0, 64, 16)])
+def test_compaction_moves_exactly_the_listed_pages(device, kv_type, D, bt):
+    """The whole pool after compaction, byte for byte: every (layer, moved
+    page) holds its source page's bytes of before the call, K and V, and
+    every other byte is unchanged (q8_0 pages move with their scale planes)."""
+    banner(f"compaction, whole-pool check, kv_type={kv_type} D={D} bt={bt}")
+    import torch
+    lens = [20 * bt + 3, 9 * bt, 31 * bt + 1, 5]
+    sc = Scenario(n_layer=3, n_head=8, n_kv=2, head_dim=D, block_tokens=bt, lens=lens,
+                  kv_type=kv_type, seed=15, extra_blocks=8, outlier_frac=0.01)
+    rng = np.random.default_rng(16)
+    for s_, n in enumerate(lens):
+        nb = -(-n // bt)
+        if nb < 2:
+            continue
+        ev = sorted(rng.choice(nb - 1, size=max(1, nb // 4), replace=False).tolist())
+        assert sc.actor.evict_blocks(s_, ev)[0]
+    ok, err, moves = sc.actor.compact()
+    assert ok and len(moves) > 0, err
+    k_old = sc.k_pool.cpu().numpy()
+    v_old = sc.v_pool.cpu().numpy()
+    emelk.copy_blocks(sc.g, sc.k_pool, sc.v_pool, torch.tensor(moves, dtype=torch.int32,
+                                                               device=device))
+    torch.cuda.synchronize()
+    pb = emelk.pool_bytes(sc.g)
+    page = pb // (sc.n_layer * sc.max_blocks)
+    mv = np.asarray(moves, np.int64).reshape(-1, 2)
+    srcs, dsts = set(mv[:, 0].tolist()), set(mv[:, 1].tolist())
+    assert not (srcs & dsts), "a move list never chains pages"
+    for old, pool in ((k_old, sc.k_pool), (v_old, sc.v_pool)):
+        want = old.reshape(sc.n_layer, sc.max_blocks, page).copy()
+        for src, dst in mv:
+            want[:, dst] = old.reshape(sc.n_layer, sc.max_blocks, page)[:, src]
+        np.testing.assert_array_equal(pool.cpu().numpy().reshape(want.shape), want)
+
+
 def test_copy_block_callback_splits_shared_tail(device):
     banner("copy_block callback through allocate_slots")
     import ctypes
