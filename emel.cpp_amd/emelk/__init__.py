@@ -145,6 +145,38 @@ NORMAL_PAIRING = (2, 2, 1, 0)
 NEOX_PAIRING = (1, 1, 0, 1)
 
 
+# Batch planner (src/emel/batch/planner/): modes, limits and error bits.
+PLAN_SIMPLE, PLAN_EQUAL, PLAN_SEQUENTIAL = 0, 1, 2
+PLAN_MAX_STEPS = 4096
+PLAN_SEQ_WORDS = 4
+PLAN_ERR = {
+    "invalid_request": 1 << 0, "invalid_token_data": 1 << 1, "invalid_step_size": 1 << 2,
+    "invalid_sequence_metadata": 1 << 3, "invalid_sequence_id": 1 << 4,
+    "invalid_sequence_mask": 1 << 5, "multiple_bits_in_mask": 1 << 6, "invalid_mode": 1 << 8,
+    "output_plan_full": 1 << 9, "output_indices_full": 1 << 10, "output_steps_full": 1 << 11,
+    "planning_progress_stalled": 1 << 12, "algorithm_failed": 1 << 13,
+    "internal_error": 1 << 15,
+}
+
+
+class PlanRequest(ctypes.Structure):
+    _fields_ = [("token_ids", c_i32p), ("n_tokens", ctypes.c_int32),
+                ("n_steps", ctypes.c_int32), ("mode", ctypes.c_int32),
+                ("seq_masks", ctypes.POINTER(ctypes.c_uint64)), ("seq_masks_count", ctypes.c_int32),
+                ("seq_primary_ids", c_i32p), ("seq_primary_ids_count", ctypes.c_int32),
+                ("equal_sequential", ctypes.c_int32), ("seq_mask_words", ctypes.c_int32),
+                ("output_mask", ctypes.POINTER(ctypes.c_int8)), ("output_mask_count", ctypes.c_int32),
+                ("output_all", ctypes.c_int32)]
+
+
+class PlanResult(ctypes.Structure):
+    _fields_ = [("step_count", ctypes.c_int32), ("total_outputs", ctypes.c_int32),
+                ("token_indices_count", ctypes.c_int32),
+                ("step_sizes", ctypes.c_int32 * PLAN_MAX_STEPS),
+                ("step_token_indices", ctypes.c_int32 * PLAN_MAX_STEPS),
+                ("step_token_offsets", ctypes.c_int32 * (PLAN_MAX_STEPS + 1))]
+
+
 # (name, restype, argtypes) for every symbol include/emelk.h declares.
 _P = ctypes.c_void_p
 _SIGNATURES = [
@@ -215,6 +247,14 @@ _SIGNATURES = [
     ("emelk_kv_cache_stream", _P, [_P]),
     ("emelk_kv_cache_copy_block", ctypes.c_bool,
      [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _P, c_i32p]),
+    ("emelk_batch_plan", ctypes.c_bool,
+     [ctypes.POINTER(PlanRequest), ctypes.POINTER(PlanResult), ctypes.POINTER(ctypes.c_uint32)]),
+    ("emelk_batch_plan_mode", ctypes.c_bool,
+     [ctypes.POINTER(PlanRequest), ctypes.c_int32, ctypes.POINTER(PlanResult),
+      ctypes.POINTER(ctypes.c_uint32)]),
+    ("emelk_plan_step_sequences", ctypes.c_uint32,
+     [ctypes.POINTER(PlanRequest), ctypes.POINTER(PlanResult), ctypes.c_int32, c_i32p, c_i32p,
+      c_i32p]),
     ("emelk_build_info", ctypes.c_char_p, []),
 ]
 SYMBOLS = [s[0] for s in _SIGNATURES]
@@ -560,3 +600,66 @@ class DevPtr:
 
     def data_ptr(self):
         return self.address
+
+
+class BatchPlan:
+    """The batch planner's process_event (src/emel/batch/planner/sm.hpp:128-134)
+    on host arrays: ``BatchPlan(token_ids, n_steps, mode, ...)`` runs it and
+    keeps ``accepted``, ``error`` (planner error bits), ``step_sizes``,
+    ``steps`` (the token indices of each step), ``total_outputs`` and
+    ``offsets``.  ``effective_step_size`` runs one mode's planner directly
+    (the mode machines' entry, with the step size given)."""
+
+    def __init__(self, token_ids, n_steps=0, mode=PLAN_SIMPLE, seq_masks=None,
+                 seq_primary_ids=None, equal_sequential=True, seq_mask_words=1,
+                 output_mask=None, output_all=False, n_tokens=None, effective_step_size=None):
+        import numpy as np
+        keep = []
+
+        def arr(x, dtype):
+            if x is None:
+                return None, 0
+            a = np.ascontiguousarray(np.asarray(x, dtype=dtype))
+            keep.append(a)
+            return a.ctypes.data_as(ctypes.POINTER(np.ctypeslib.as_ctypes_type(dtype))), \
+                (a.shape[0] if a.ndim else 1)
+
+        tok, ntok = arr(token_ids, np.int32)
+        masks, nmask = arr(seq_masks, np.uint64)
+        prim, nprim = arr(seq_primary_ids, np.int32)
+        outm, nout = arr(output_mask, np.int8)
+        if masks is not None and seq_mask_words > 0:
+            nmask //= seq_mask_words  # rows of seq_mask_words words
+        self.request = PlanRequest(tok, ntok if n_tokens is None else n_tokens, n_steps, mode,
+                                   masks, nmask, prim, nprim, int(bool(equal_sequential)),
+                                   seq_mask_words, outm, nout, int(bool(output_all)))
+        self._keep = keep
+        self.result = PlanResult()
+        err = ctypes.c_uint32(0)
+        if effective_step_size is None:
+            self.accepted = lib.emelk_batch_plan(ctypes.byref(self.request),
+                                                 ctypes.byref(self.result), ctypes.byref(err))
+        else:
+            self.accepted = lib.emelk_batch_plan_mode(ctypes.byref(self.request),
+                                                      effective_step_size,
+                                                      ctypes.byref(self.result), ctypes.byref(err))
+        self.error = err.value
+        r = self.result
+        self.step_count = r.step_count
+        self.total_outputs = r.total_outputs
+        self.token_indices_count = r.token_indices_count
+        self.step_sizes = list(r.step_sizes[:r.step_count])
+        self.offsets = list(r.step_token_offsets[:r.step_count + 1]) if r.step_count else []
+        idx = list(r.step_token_indices[:r.token_indices_count])
+        self.steps = [idx[self.offsets[i]:self.offsets[i + 1]] for i in range(r.step_count)]
+
+    def step_sequences(self, step):
+        """(seq_ids, n_tokens) of an equal-shaped step, the arguments of
+        emelk_batch_decoder_begin_step; raises if the step is not one."""
+        seq = (ctypes.c_int32 * MAX_SEQUENCES)()
+        n_seq = ctypes.c_int32(0)
+        n_tok = ctypes.c_int32(0)
+        _check(lib.emelk_plan_step_sequences(ctypes.byref(self.request), ctypes.byref(self.result),
+                                             step, seq, ctypes.byref(n_seq), ctypes.byref(n_tok)),
+               "emelk_plan_step_sequences")
+        return list(seq[:n_seq.value]), n_tok.value

@@ -394,6 +394,93 @@ emel_error_type emelk_batch_decoder_layer(emelk_batch_decoder *decoder, int32_t 
                                           const float *k_norm, int32_t v_rms, float rms_epsilon,
                                           float scale, float *out);
 
+/* ---- Batch planner (host) ----------------------------------------------
+ * Splits a batch of tokens into steps, as emel::batch::planner::sm does
+ * (src/emel/batch/planner/sm.hpp:20-146, detail.hpp:129-359,
+ * modes/{simple,equal,sequential}/actions.hpp): `simple` cuts the tokens
+ * into chunks of the step size; `sequential` grows each step along tokens
+ * whose sequence set is a subset of the current one; `equal` takes the same
+ * number of tokens from every sequence of a group of non-overlapping
+ * sequences (consecutive primary ids when equal_sequential).  An equal step
+ * is the shape emelk_batch_decoder_begin_step takes; see
+ * emelk_plan_step_sequences. */
+#define EMELK_PLAN_MAX_STEPS 4096 /* batch/planner/context.hpp:7 */
+#define EMELK_PLAN_SEQ_WORDS 4    /* 256 sequences: context.hpp:8-9 */
+
+typedef enum emelk_plan_mode {
+  EMELK_PLAN_SIMPLE = 0,
+  EMELK_PLAN_EQUAL = 1,
+  EMELK_PLAN_SEQUENTIAL = 2
+} emelk_plan_mode;
+
+/* Planner error bits (batch/planner/errors.hpp:6-24). */
+#define EMELK_PLAN_ERR_INVALID_REQUEST (1u << 0)
+#define EMELK_PLAN_ERR_INVALID_TOKEN_DATA (1u << 1)
+#define EMELK_PLAN_ERR_INVALID_STEP_SIZE (1u << 2)
+#define EMELK_PLAN_ERR_INVALID_SEQUENCE_METADATA (1u << 3)
+#define EMELK_PLAN_ERR_INVALID_SEQUENCE_ID (1u << 4)
+#define EMELK_PLAN_ERR_INVALID_SEQUENCE_MASK (1u << 5)
+#define EMELK_PLAN_ERR_MULTIPLE_BITS_IN_MASK (1u << 6)
+#define EMELK_PLAN_ERR_INVALID_MODE (1u << 8)
+#define EMELK_PLAN_ERR_OUTPUT_PLAN_FULL (1u << 9)
+#define EMELK_PLAN_ERR_OUTPUT_INDICES_FULL (1u << 10)
+#define EMELK_PLAN_ERR_OUTPUT_STEPS_FULL (1u << 11)
+#define EMELK_PLAN_ERR_PLANNING_PROGRESS_STALLED (1u << 12)
+#define EMELK_PLAN_ERR_ALGORITHM_FAILED (1u << 13)
+#define EMELK_PLAN_ERR_INTERNAL_ERROR (1u << 15)
+
+/* event::plan_request (batch/planner/events.hpp:20-41) without the
+ * callbacks.  seq_masks: n_tokens rows of seq_mask_words uint64 words (bit s
+ * = sequence s); seq_primary_ids: one sequence id per token; with neither,
+ * every token is on sequence 0.  The reference's default seq_mask_words is
+ * 1 and equal_sequential true. */
+typedef struct emelk_plan_request {
+  const int32_t *token_ids;
+  int32_t n_tokens;
+  int32_t n_steps;  /* step size; <= 0 means n_tokens */
+  int32_t mode;     /* emelk_plan_mode */
+  const uint64_t *seq_masks;
+  int32_t seq_masks_count;
+  const int32_t *seq_primary_ids;
+  int32_t seq_primary_ids_count;
+  int32_t equal_sequential;
+  int32_t seq_mask_words;
+  const int8_t *output_mask;
+  int32_t output_mask_count;
+  int32_t output_all;
+} emelk_plan_request;
+
+/* events::plan_done (events.hpp:62-71): step s holds the token indices
+ * step_token_indices[step_token_offsets[s] .. step_token_offsets[s+1]) and
+ * has step_sizes[s] of them.  Counts are zero after a refused request. */
+typedef struct emelk_plan_result {
+  int32_t step_count;
+  int32_t total_outputs;
+  int32_t token_indices_count;
+  int32_t step_sizes[EMELK_PLAN_MAX_STEPS];
+  int32_t step_token_indices[EMELK_PLAN_MAX_STEPS];
+  int32_t step_token_offsets[EMELK_PLAN_MAX_STEPS + 1];
+} emelk_plan_result;
+
+/* The planner's process_event: true iff a plan was produced; *error_out
+ * (optional) receives the error bits (0 on success).  Replaces
+ * Planner::process_event (batch/planner/sm.hpp:128-134). */
+bool emelk_batch_plan(const emelk_plan_request *request, emelk_plan_result *result,
+                      uint32_t *error_out);
+/* One mode's planner with the step size given (modes::*::sm with
+ * plan_scratch::effective_step_size set by the caller), without the outer
+ * input validation and step-size normalisation. */
+bool emelk_batch_plan_mode(const emelk_plan_request *request, int32_t effective_step_size,
+                           emelk_plan_result *result, uint32_t *error_out);
+/* The decoder shape of plan step `step`: its tokens must form runs of one
+ * sequence each, all runs of equal length (what `equal` produces, and any
+ * single-sequence step).  Writes the run sequences in order to seq_ids_out
+ * (capacity EMELK_MAX_SEQUENCES) and the run length to *n_tokens_out. */
+emel_error_type emelk_plan_step_sequences(const emelk_plan_request *request,
+                                          const emelk_plan_result *result, int32_t step,
+                                          int32_t *seq_ids_out, int32_t *n_seq_out,
+                                          int32_t *n_tokens_out);
+
 /* Library version and the device the kernels were built for. */
 const char *emelk_build_info(void);
 

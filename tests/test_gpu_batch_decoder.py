@@ -154,3 +154,64 @@ def test_batch_decoder_requires_the_cache_stream(device):
     with pytest.raises(RuntimeError):
         emelk.BatchDecoder(g, actor, cache, rope, max_batch=2, max_kv_len=64,
                            stream=other.cuda_stream)
+
+
+@pytest.mark.parametrize("kv_type", [emelk.KV_F16, emelk.KV_Q8_0])
+def test_batch_decoder_runs_an_equal_plan(device, kv_type):
+    """Prompts of three sequences, their tokens interleaved in one batch,
+    planned by the batch planner in equal mode (the same number of tokens
+    from every sequence of a step, each sequence's tokens in order) and run
+    step by step through the executor: each step's (sequences, tokens per
+    sequence) is emelk_plan_step_sequences of the plan."""
+    import torch
+    banner(f"batch decoder driven by an equal-mode plan, kv_type={kv_type}")
+    rng = np.random.default_rng(11)
+    lens = [13, 7, 20]
+    ids = np.concatenate([np.full(n, s, np.int32) for s, n in enumerate(lens)])
+    rng.shuffle(ids)
+    n = len(ids)
+    plan = emelk.BatchPlan(rng.integers(0, 32000, size=n).astype(np.int32), n_steps=9,
+                           mode=emelk.PLAN_EQUAL, seq_primary_ids=ids, equal_sequential=False,
+                           output_all=True)
+    assert plan.accepted, plan.error
+    g = emelk.geometry(L, H, HKV, D, BT, 32, kv_type)
+    actor = emelk.KvActor()
+    assert actor.reserve(4, 32, BT)[0]
+    actor.set_free_order(rng.permutation(32).astype(np.uint16))
+    for s in range(3):
+        assert actor.allocate_sequence(s)[0]
+    cache = emelk.KvCache(g)
+    rope = emelk.RopeTable(D, D, 64, BASE, emelk.NEOX_PAIRING)
+    dec = emelk.BatchDecoder(g, actor, cache, rope, max_batch=3, max_kv_len=64)
+    model = Model(kv_type)
+    for s in range(3):
+        model.ensure(s)
+    # per token and layer: the projection rows
+    q = rng.standard_normal((L, n, H * D)).astype(np.float32)
+    k = rng.standard_normal((L, n, HKV * D)).astype(np.float32)
+    v = rng.standard_normal((L, n, HKV * D)).astype(np.float32)
+    shapes = []
+    for step, tokens in enumerate(plan.steps):
+        seqs, per = plan.step_sequences(step)
+        shapes.append((tuple(seqs), per))
+        pos = dec.begin_step(seqs, per)
+        order = np.array(tokens).reshape(len(seqs), per)
+        for i, s in enumerate(seqs):
+            assert pos[i] == len(model.k[s][0])
+            assert all(ids[t] == s for t in order[i])
+        for layer in range(L):
+            qd = torch.from_numpy(q[layer][order]).to(device)
+            out = torch.full(qd.shape, float("nan"), device=device)
+            dec.layer(layer, qd, qd, torch.from_numpy(k[layer][order]).to(device),
+                      torch.from_numpy(v[layer][order]).to(device), out, SCALE)
+            torch.cuda.synchronize()
+            got = out.cpu().numpy()
+            for i, s in enumerate(seqs):
+                for j, t in enumerate(order[i]):
+                    want = model.token(s, layer, q[layer, t], k[layer, t], v[layer, t],
+                                       pos[i] + j, None, None)
+                    assert_close(got[i, j], want, what=f"step {step} layer {layer} seq {s} tok {t}")
+    assert [len(model.k[s][0]) for s in range(3)] == lens
+    # the plan mixes multi-sequence prefill steps with steps of other shapes
+    assert any(len(sq) == 3 for sq, _ in shapes) and any(p > 1 for _, p in shapes)
+    dec.close()
