@@ -191,35 +191,38 @@ void plan_simple(plan_state &S) {
 // sequential (modes/sequential/actions.hpp:30-92): a step starts at the
 // first unused token and takes, in order, unused tokens whose sequence set
 // lies inside the set of the token taken before them, up to `step` tokens.
+// Unused tokens are kept in a linked list in token order, so a step's
+// search skips the tokens earlier steps took.
 void plan_sequential(plan_state &S) {
   const int32_t n = S.rq.n_tokens;
-  std::vector<uint8_t> used(static_cast<size_t>(n), 0);
-  int32_t n_used = 0;
-  int32_t first_free = 0;
-  while (n_used < n) {
-    while (first_free < n && used[first_free] != 0) ++first_free;
-    if (first_free >= n) break;
-    int32_t cur = first_free;
-    seq_mask cur_mask = S.mask_of(cur);
+  std::vector<seq_mask> masks(static_cast<size_t>(n));
+  for (int32_t i = 0; i < n; ++i) masks[i] = S.mask_of(i);
+  // doubly linked list of the unused tokens in token order; node n is the
+  // sentinel (next[n] is the first unused token, n when none is left)
+  std::vector<int32_t> next(static_cast<size_t>(n) + 1), prev(static_cast<size_t>(n) + 1);
+  for (int32_t i = 0; i <= n; ++i) {
+    next[i] = i == n ? (n > 0 ? 0 : n) : (i + 1 < n ? i + 1 : n);
+    prev[i] = i == n ? (n > 0 ? n - 1 : n) : (i > 0 ? i - 1 : n);
+  }
+  auto unlink = [&](int32_t i) {
+    next[prev[i]] = next[i];
+    prev[next[i]] = prev[i];
+  };
+  while (next[n] != n) {
+    int32_t cur = next[n];  // first unused token
+    seq_mask cur_mask = masks[cur];
     if (!S.open_step()) return S.fail(EMELK_PLAN_ERR_OUTPUT_STEPS_FULL);
     int32_t taken = 0;
     for (;;) {
-      used[cur] = 1;
-      ++n_used;
+      int32_t after = next[cur];
+      unlink(cur);
       ++taken;
       if (!S.add_token(cur)) return S.fail(EMELK_PLAN_ERR_OUTPUT_INDICES_FULL);
       if (taken >= S.step) break;
-      int32_t next = cur + 1;
-      for (; next < n; ++next) {
-        if (used[next] != 0) continue;
-        const seq_mask m = S.mask_of(next);
-        if (contains(cur_mask, m)) {
-          cur_mask = m;
-          break;
-        }
-      }
-      if (next >= n) break;
-      cur = next;
+      while (after != n && !contains(cur_mask, masks[after])) after = next[after];
+      if (after == n) break;
+      cur = after;
+      cur_mask = masks[cur];
     }
     if (!S.close_step(taken)) return S.fail(EMELK_PLAN_ERR_OUTPUT_STEPS_FULL);
   }
@@ -231,57 +234,74 @@ void plan_sequential(plan_state &S) {
 // equal_sequential and primary ids, each next primary id one above the
 // last; the scan stops once the group has one more member than the step
 // size, which then leaves no room and stalls), then takes the same number
-// of tokens, min(step / group size, fewest available), from every member.
+// of tokens, min(step / group size, fewest available), from every member,
+// each member's earliest unused tokens first.  Tokens are bucketed by
+// their exact set: a member's tokens are then the next ones of its bucket,
+// and a token clashes with the group iff it meets the union of its sets.
 void plan_equal_general(plan_state &S) {
   const int32_t n = S.rq.n_tokens;
-  std::vector<uint8_t> used(static_cast<size_t>(n), 0);
   std::vector<seq_mask> masks(static_cast<size_t>(n));
   for (int32_t i = 0; i < n; ++i) masks[i] = S.mask_of(i);
-  std::vector<seq_mask> group;
-  group.reserve(static_cast<size_t>(std::min(n, S.step + 1)));
+  // buckets of equal sets, each a list of token indices in order
+  std::vector<int32_t> bucket_of(static_cast<size_t>(n));
+  std::vector<std::vector<int32_t>> buckets;
+  std::vector<seq_mask> bucket_mask;
+  {
+    std::vector<int32_t> order(static_cast<size_t>(n));
+    for (int32_t i = 0; i < n; ++i) order[i] = i;
+    std::stable_sort(order.begin(), order.end(),
+                     [&](int32_t x, int32_t y) { return masks[x] < masks[y]; });
+    for (int32_t k = 0; k < n; ++k) {
+      const int32_t i = order[k];
+      if (k == 0 || masks[i] != masks[order[k - 1]]) {
+        buckets.emplace_back();
+        bucket_mask.push_back(masks[i]);
+      }
+      bucket_of[i] = static_cast<int32_t>(buckets.size()) - 1;
+      buckets.back().push_back(i);  // ascending: stable over token order
+    }
+  }
+  std::vector<int32_t> cursor(buckets.size(), 0);
+  std::vector<uint8_t> used(static_cast<size_t>(n), 0);
+  std::vector<int32_t> group;
   int32_t n_used = 0;
   while (n_used < n) {
     group.clear();
+    seq_mask taken_bits{};
     int32_t last_primary = -1;
     for (int32_t i = 0; i < n; ++i) {
-      if (used[i] != 0) continue;
-      bool clash = false;
-      for (const seq_mask &g : group) {
-        if (overlaps(g, masks[i])) {
-          clash = true;
-          break;
-        }
-      }
-      if (clash) continue;
+      if (used[i] != 0 || overlaps(taken_bits, masks[i])) continue;
       if (S.rq.equal_sequential != 0 && S.rq.seq_primary_ids != nullptr) {
         const int32_t primary = S.rq.seq_primary_ids[i];
         if (!group.empty() && primary != last_primary + 1) continue;
         last_primary = primary;
       }
-      group.push_back(masks[i]);
+      group.push_back(bucket_of[i]);
+      for (int32_t w = 0; w < k_words; ++w) taken_bits[w] |= masks[i][w];
       if (static_cast<int32_t>(group.size()) > S.step) break;
     }
     const int32_t n_groups = static_cast<int32_t>(group.size());
     if (n_groups == 0) return S.fail(EMELK_PLAN_ERR_PLANNING_PROGRESS_STALLED);
     int32_t fewest = n + 1;
-    for (const seq_mask &g : group) {
-      int32_t avail = 0;
-      for (int32_t i = 0; i < n; ++i) avail += (used[i] == 0 && masks[i] == g) ? 1 : 0;
-      fewest = std::min(fewest, avail);
+    for (int32_t b : group) {
+      fewest = std::min(fewest, static_cast<int32_t>(buckets[b].size()) - cursor[b]);
     }
     const int32_t per_seq = std::min(S.step / n_groups, fewest);
     if (per_seq <= 0) return S.fail(EMELK_PLAN_ERR_PLANNING_PROGRESS_STALLED);
     if (!S.open_step()) return S.fail(EMELK_PLAN_ERR_OUTPUT_STEPS_FULL);
-    for (const seq_mask &g : group) {
-      int32_t left = per_seq;
-      for (int32_t i = 0; i < n && left > 0; ++i) {
-        if (used[i] != 0 || masks[i] != g) continue;
+    for (int32_t b : group) {
+      // members with the same set (possible only for an empty set, which
+      // the request checks refuse) share a bucket and may run it dry
+      if (cursor[b] + per_seq > static_cast<int32_t>(buckets[b].size())) {
+        return S.fail(EMELK_PLAN_ERR_ALGORITHM_FAILED);
+      }
+      for (int32_t k = 0; k < per_seq; ++k) {
+        const int32_t i = buckets[b][cursor[b] + k];
         used[i] = 1;
         ++n_used;
         if (!S.add_token(i)) return S.fail(EMELK_PLAN_ERR_OUTPUT_INDICES_FULL);
-        --left;
       }
-      if (left != 0) return S.fail(EMELK_PLAN_ERR_ALGORITHM_FAILED);
+      cursor[b] += per_seq;
     }
     if (!S.close_step(per_seq * n_groups)) return S.fail(EMELK_PLAN_ERR_OUTPUT_STEPS_FULL);
   }

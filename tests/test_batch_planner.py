@@ -277,3 +277,77 @@ def test_step_sequences_rejects_mixed_steps():
         r.step_sequences(0)
     with pytest.raises(RuntimeError):
         q.step_sequences(1)
+
+
+# ---- the bucketed / linked-list passes against the step rules written out
+# token by token (modes/sequential/actions.hpp:30-92, modes/equal/
+# actions.hpp:34-139), on seeded batches with multi-sequence masks ----------
+
+def _sequential_rules(masks, step):
+    n = len(masks)
+    used = [False] * n
+    steps = []
+    while not all(used):
+        cur = used.index(False)
+        cur_mask = masks[cur]
+        cur_step = []
+        while True:
+            used[cur] = True
+            cur_step.append(cur)
+            if len(cur_step) >= step:
+                break
+            nxt = next((j for j in range(cur + 1, n)
+                        if not used[j] and (cur_mask & masks[j]) == masks[j]), None)
+            if nxt is None:
+                break
+            cur, cur_mask = nxt, masks[nxt]
+        steps.append(cur_step)
+    return steps
+
+
+def _equal_rules(masks, step):
+    n = len(masks)
+    used = [False] * n
+    steps = []
+    while not all(used):
+        group = []
+        for i in range(n):
+            if used[i] or any(g & masks[i] for g in group):
+                continue
+            group.append(masks[i])
+            if len(group) > step:
+                break
+        fewest = min(sum(1 for i in range(n) if not used[i] and masks[i] == g) for g in group)
+        per = min(step // len(group), fewest)
+        if per <= 0:
+            return None
+        cur_step = []
+        for g in group:
+            take = [i for i in range(n) if not used[i] and masks[i] == g][:per]
+            for i in take:
+                used[i] = True
+            cur_step.extend(take)
+        steps.append(cur_step)
+    return steps
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_fast_passes_follow_the_step_rules(seed):
+    rng = np.random.default_rng(100 + seed)
+    n = int(rng.integers(1, 300))
+    n_seq = int(rng.integers(1, 12))
+    step = int(rng.integers(1, 40))
+    # sequential: arbitrary non-empty sets over n_seq sequences
+    masks = rng.integers(1, 1 << n_seq, size=n).astype(np.uint64)
+    p = plan(np.arange(n, dtype=np.int32), n_steps=step, mode=PLAN_SEQUENTIAL, seq_masks=masks)
+    assert p.accepted and p.steps == _sequential_rules([int(m) for m in masks], min(step, n))
+    # equal (general path): disjoint sets, a few sequences sharing tokens
+    groups = [1 << s for s in range(n_seq)] + [3 << (2 * k) for k in range(n_seq // 2)]
+    masks = np.array([groups[j] for j in rng.integers(0, len(groups), size=n)], np.uint64)
+    p = plan(np.arange(n, dtype=np.int32), n_steps=step, mode=PLAN_EQUAL, seq_masks=masks,
+             equal_sequential=False)
+    want = _equal_rules([int(m) for m in masks], min(step, n))
+    if want is None:
+        assert not p.accepted and p.error == E["planning_progress_stalled"]
+    else:
+        assert p.accepted and p.steps == want
