@@ -34,12 +34,18 @@ sys.path.insert(0, os.path.join(ROOT, "emel.cpp_amd"))
 
 HBM_PEAK_GBS = 8000.0
 
-# HBM bytes per decode_kernel launch on the default workload, from the two
-# rocprofv3 PMC runs (FETCH_SIZE, WRITE_SIZE) summarised in
-# profiles/decode_kernel_llama3-8b-b64-ctx8k.md, each scaled by the same
-# counter's reading on a plain 1 GiB copy (bench.py --copy-calibration):
-# FETCH_SIZE x2.000, WRITE_SIZE x1.000.
-PMC_TRAFFIC_BYTES = {"llama3-8b-b64-ctx8k": 2157387464}
+# HBM bytes per launch of the measured kernels (decode_kernel + combine_kernel
+# per layer for decode, prefill_kernel per layer for the chunked prefill),
+# from the two rocprofv3 PMC runs (FETCH_SIZE, WRITE_SIZE) summarised in the
+# profiles/ file of each workload, each scaled by the same counter's reading
+# on a plain 1 GiB copy (bench.py --copy-calibration): FETCH_SIZE x2.000,
+# WRITE_SIZE x1.000.
+PMC_TRAFFIC_BYTES = {
+    "llama3-8b-b64-ctx8k": 2157387464,
+    "llama3-8b-q8_0-b32-ctx16k": 1155282739,
+    "llama3-8b-prefill512-evict25": 285551820,
+    "llama3-8b-q8_0-prefill512-evict25": 214867558,
+}
 
 CONFIGS = {
     # name: (n_layer, n_head, n_kv, head_dim, block_tokens, batch, ctx, kv_type)
@@ -394,6 +400,10 @@ def prefill_evict(args, torch, emelk, dev):
     torch.cuda.synchronize()
     ms_step = 1e3 * (time.perf_counter() - t0) / K
     attn_ms = float(np.mean([e[0].elapsed_time(e[1]) for row in ev for e in row]))
+    # bytes the kernel must move per launch: the unique K/V of the layer
+    # (prefix + chunk, every KV head), the fp32 queries and the fp32 output
+    prefill_bytes = (B * HK * (P0 + NQ) * (page_bytes // (HK * BT)) * 2
+                     + 2 * B * NQ * H * D * 4)
     rows = np.arange(NQ, dtype=np.float64)
     flops_layer = 4.0 * D * H * B * float(np.sum(P0 + rows + 1))
     tflops = flops_layer / (attn_ms * 1e-3) / 1e12
@@ -425,7 +435,9 @@ def prefill_evict(args, torch, emelk, dev):
         "config": {"workload": args.config, "batch": B, "prefix": P0,
                    "chunk": NQ, "n_layer": L, "block_tokens": BT},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": 2500.0,
-                     "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4), "traffic": None,
+                     "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4),
+                     "traffic": PMC_TRAFFIC_BYTES.get(args.config),
+                     "algorithmic_bytes": prefill_bytes,
                      "kernel": "prefill_kernel (HIP events per layer call)",
                      "flops_per_launch": flops_layer, "avg_launch_ms": round(attn_ms, 4)},
         "compaction": {"pages_evicted": evicted, "moves": len(moves), "ms": round(copy_ms, 4),
