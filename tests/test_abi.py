@@ -87,3 +87,18 @@ def test_rope_table_rejects_bad_pairings_before_touching_the_gpu():
     assert emelk.lib.emelk_kv_qkv_rope_append(ctypes.byref(g), None, None, 0, None, None, None,
                                               None, 1, 1, None, None, 1, None, None, None, 0,
                                               1e-6, None) == emelk.ERR_INVALID_REQUEST
+
+
+def test_plain_c_client_builds_and_runs(tmp_path):
+    """include/emelk.h compiles as C11 with warnings as errors, and a C
+    program linked against libemelk.so drives the actor through the
+    kv_binding table and plans prompts (tests/cpp/abi_consumer.c)."""
+    import subprocess
+    exe = str(tmp_path / "abi_consumer")
+    libdir = os.path.dirname(emelk.LIB_PATH)
+    subprocess.run(["gcc", "-std=c11", "-Wall", "-Wextra", "-Werror", "-I",
+                    os.path.join(ROOT, "include"), os.path.join(ROOT, "tests", "cpp",
+                                                                "abi_consumer.c"),
+                    "-L", libdir, "-lemelk", f"-Wl,-rpath,{libdir}", "-o", exe], check=True)
+    res = subprocess.run([exe], capture_output=True, text=True, timeout=60)
+    assert res.returncode == 0 and res.stdout.strip() == "ok", res.stdout + res.stderr
