@@ -68,6 +68,7 @@ def main():
     ap.add_argument("--config", default="llama3-8b-b64-ctx8k",
                     choices=sorted(CONFIGS) + ["llama3-8b-prefill512-evict25",
                                                "llama3-8b-q8_0-prefill512-evict25",
+                                               "gemma4-d256-prefill512-evict25",
                                                "llama3-8b-b64-ctx8k-generator"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--separate-append", action="store_true",
@@ -99,7 +100,8 @@ def main():
         return
     import emelk
 
-    if args.config in ("llama3-8b-prefill512-evict25", "llama3-8b-q8_0-prefill512-evict25"):
+    if args.config in ("llama3-8b-prefill512-evict25", "llama3-8b-q8_0-prefill512-evict25",
+                       "gemma4-d256-prefill512-evict25"):
         return prefill_evict(args, torch, emelk, dev)
     if args.config == "llama3-8b-b64-ctx8k-generator":
         return generator(args, torch, emelk, dev)
@@ -334,6 +336,10 @@ def prefill_evict(args, torch, emelk, dev):
     through the quantizing append; K/V are dequantized to fp16 while staged
     for the MFMAs)."""
     L, H, HK, D, BT, B, P0, NQ = 32, 32, 8, 128, 32, 8, 4096, 512
+    if args.config.startswith("gemma4-d256"):
+        # Gemma-4's sliding-window attention layers: 8 query heads on one KV
+        # head of 256 (src/emel/model/gemma4/detail.cpp:24-29); 8 layers
+        L, H, HK, D = 8, 8, 1, 256
     q8 = "q8_0" in args.config
     rng = np.random.default_rng(args.seed)
     total = P0 + NQ

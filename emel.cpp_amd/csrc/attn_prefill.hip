@@ -715,19 +715,27 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
 
 template <int D, int KT, bool Q8>
 bool launch_prefill_kt(const prefill_params &P, int32_t n_seq, hipStream_t st) {
-  // 8 waves per workgroup: G_WG query heads of one KV group x RB blocks of
-  // 32 query rows, all sharing each staged K/V tile.
+  // W waves per workgroup: G_WG query heads of one KV group x RB blocks of
+  // 32 query rows, all sharing each staged K/V tile.  head_dim 256 runs 4
+  // waves, one per SIMD, so each has the full register file for its 32 x
+  // 256 O tile and Q^T operand (8 waves at head_dim <= 128).
+  constexpr int W = D > 128 ? 4 : 8;
   const int group = P.L.n_head / P.L.n_head_kv;
-  const int g_wg = group < 8 ? group : 8;
-  const int rb = 8 / g_wg;
+  const int g_wg = group < W ? group : W;
+  const int rb = W / g_wg;
   const int n_qt = (P.n_q + 32 * rb - 1) / (32 * rb);
   const dim3 grid(n_qt * (P.L.n_head / g_wg) * n_seq);
-  const dim3 block(8 * k_wave);
+  const dim3 block(W * k_wave);
   switch (g_wg) {
-    case 1: hipLaunchKernelGGL((prefill_kernel<D, 1, 8, KT, Q8>), grid, block, 0, st, P); return true;
-    case 2: hipLaunchKernelGGL((prefill_kernel<D, 2, 4, KT, Q8>), grid, block, 0, st, P); return true;
-    case 4: hipLaunchKernelGGL((prefill_kernel<D, 4, 2, KT, Q8>), grid, block, 0, st, P); return true;
-    case 8: hipLaunchKernelGGL((prefill_kernel<D, 8, 1, KT, Q8>), grid, block, 0, st, P); return true;
+    case 1: hipLaunchKernelGGL((prefill_kernel<D, 1, W, KT, Q8>), grid, block, 0, st, P); return true;
+    case 2: hipLaunchKernelGGL((prefill_kernel<D, 2, W / 2, KT, Q8>), grid, block, 0, st, P); return true;
+    case 4: hipLaunchKernelGGL((prefill_kernel<D, 4, W / 4, KT, Q8>), grid, block, 0, st, P); return true;
+    case 8:
+      if constexpr (W == 8) {
+        hipLaunchKernelGGL((prefill_kernel<D, 8, 1, KT, Q8>), grid, block, 0, st, P);
+        return true;
+      }
+      return false;
     default: return false;
   }
 }
@@ -761,10 +769,10 @@ extern "C" emel_error_type emelk_attn_prefill_chunk(const emelk_kv_geometry *g, 
       !std::isfinite(scale)) {
     return EMELK_ERR_INVALID_REQUEST;
   }
-  if (L.head_dim > 128) {
-    // head_dim 256 / 512 (whose O and Q^T tiles do not fit this kernel's
-    // registers): row by row through the decode kernel, as the reference's
-    // per-row loop does
+  if (L.head_dim == 512 || (L.head_dim == 256 && L.kv_type == EMELK_KV_Q8_0)) {
+    // head_dim 512 (whose O and Q^T tiles do not fit one wave's registers)
+    // and q8_0 at 256 (whose hi/lo planes do not fit the LDS): row by row
+    // through the decode kernel, as the reference's per-row loop does
     return emelk::decode_rows(L, k_pool, v_pool, layer, q, out, n_seq, n_q, q_start,
                               block_tables, table_stride, scale, static_cast<hipStream_t>(stream));
   }
@@ -785,8 +793,9 @@ extern "C" emel_error_type emelk_attn_prefill_chunk(const emelk_kv_geometry *g, 
     if ((1 << b) == L.block_tokens) P.bt_shift = b;
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const bool ok = L.head_dim == 128 ? emelk::launch_prefill<128>(P, n_seq, st)
-                                    : emelk::launch_prefill<64>(P, n_seq, st);
+  const bool ok = L.head_dim == 256   ? emelk::launch_prefill_kt<256, 32, false>(P, n_seq, st)
+                  : L.head_dim == 128 ? emelk::launch_prefill<128>(P, n_seq, st)
+                                      : emelk::launch_prefill<64>(P, n_seq, st);
   if (!ok) return EMELK_ERR_INVALID_REQUEST;
   return hipGetLastError() == hipSuccess ? EMELK_ERR_NONE : EMELK_ERR_BACKEND;
 }

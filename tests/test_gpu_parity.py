@@ -687,6 +687,7 @@ Q8_PREFILL_CASES = [
     (16, 2, 64, 8, [19, 0], 40, None),            # G=8, pages of 8
     (8, 2, 128, 32, [100, 37], 40, (0, 1)),       # NaN-filled pool, an invalid page
     (8, 2, 128, 16, [100, 37], 40, (1, 2)),
+    (8, 1, 256, 16, [40], 9, None),               # head_dim 256: row by row
 ]
 
 
@@ -794,7 +795,20 @@ def test_decode_append_large_heads(device):
                                           err_msg=f"{which} pool D={D}")
 
 
-def test_prefill_chunk_large_heads(device):
-    # head_dim 256 takes the row-by-row route through the decode kernel
-    banner("prefill chunk at head_dim 256 (row by row)")
-    _prefill_case(device, 8, 2, 256, 16, [0, 130], 21, seed=81)
+@pytest.mark.parametrize("n_head,n_kv,bt,q_starts,n_q", [
+    (8, 2, 16, [0, 130], 21),      # G=4, general staging (pages of 16)
+    (8, 8, 32, [33], 70),          # G=1: 4 row blocks per workgroup
+    (8, 4, 32, [100, 0], 45),      # G=2
+    (16, 2, 32, [64], 40),         # G=8: two workgroups per KV head
+])
+def test_prefill_chunk_head_dim_256(device, n_head, n_kv, bt, q_starts, n_q):
+    """head_dim 256 (Gemma-4 sliding-window layers) on the MFMA kernel: 4
+    waves per workgroup, 32-key tiles."""
+    banner(f"prefill chunk at head_dim 256 H={n_head}/{n_kv} bt={bt} starts={q_starts} n_q={n_q}")
+    _prefill_case(device, n_head, n_kv, 256, bt, q_starts, n_q, seed=81)
+
+
+def test_prefill_chunk_head_dim_512_row_route(device):
+    # head_dim 512 takes the row-by-row route through the decode kernel
+    banner("prefill chunk at head_dim 512 (row by row)")
+    _prefill_case(device, 8, 2, 512, 16, [0, 70], 13, seed=82)
