@@ -69,6 +69,7 @@ def main():
                     choices=sorted(CONFIGS) + ["llama3-8b-prefill512-evict25",
                                                "llama3-8b-q8_0-prefill512-evict25",
                                                "gemma4-d256-prefill512-evict25",
+                                               "gemma4-d256-q8_0-prefill512-evict25",
                                                "llama3-8b-b64-ctx8k-generator"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--separate-append", action="store_true",
@@ -101,7 +102,7 @@ def main():
     import emelk
 
     if args.config in ("llama3-8b-prefill512-evict25", "llama3-8b-q8_0-prefill512-evict25",
-                       "gemma4-d256-prefill512-evict25"):
+                       "gemma4-d256-prefill512-evict25", "gemma4-d256-q8_0-prefill512-evict25"):
         return prefill_evict(args, torch, emelk, dev)
     if args.config == "llama3-8b-b64-ctx8k-generator":
         return generator(args, torch, emelk, dev)

@@ -769,10 +769,10 @@ extern "C" emel_error_type emelk_attn_prefill_chunk(const emelk_kv_geometry *g, 
       !std::isfinite(scale)) {
     return EMELK_ERR_INVALID_REQUEST;
   }
-  if (L.head_dim == 512 || (L.head_dim == 256 && L.kv_type == EMELK_KV_Q8_0)) {
-    // head_dim 512 (whose O and Q^T tiles do not fit one wave's registers)
-    // and q8_0 at 256 (whose hi/lo planes do not fit the LDS): row by row
-    // through the decode kernel, as the reference's per-row loop does
+  if (L.head_dim == 512) {
+    // head_dim 512 (whose O and Q^T tiles do not fit one wave's registers):
+    // row by row through the decode kernel, as the reference's per-row loop
+    // does
     return emelk::decode_rows(L, k_pool, v_pool, layer, q, out, n_seq, n_q, q_start,
                               block_tables, table_stride, scale, static_cast<hipStream_t>(stream));
   }
@@ -793,7 +793,12 @@ extern "C" emel_error_type emelk_attn_prefill_chunk(const emelk_kv_geometry *g, 
     if ((1 << b) == L.block_tokens) P.bt_shift = b;
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const bool ok = L.head_dim == 256   ? emelk::launch_prefill_kt<256, 32, false>(P, n_seq, st)
+  const bool q8 = L.kv_type == EMELK_KV_Q8_0;
+  // head_dim 256: 32-key tiles (64 spill, and q8_0's hi/lo planes of 64-key
+  // tiles would not fit the LDS)
+  const bool ok = L.head_dim == 256
+                      ? (q8 ? emelk::launch_prefill_kt<256, 32, true>(P, n_seq, st)
+                            : emelk::launch_prefill_kt<256, 32, false>(P, n_seq, st))
                   : L.head_dim == 128 ? emelk::launch_prefill<128>(P, n_seq, st)
                                       : emelk::launch_prefill<64>(P, n_seq, st);
   if (!ok) return EMELK_ERR_INVALID_REQUEST;

@@ -1,5 +1,5 @@
 // Per-row chunked prefill through the decode kernel (attn_decode.hip), used
-// for the head sizes the MFMA prefill kernel does not take (256 and 512).
+// for the head size the MFMA prefill kernel does not take (512).
 #pragma once
 
 #include <hip/hip_runtime.h>

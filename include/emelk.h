@@ -281,10 +281,9 @@ emel_error_type emelk_attn_decode_append(const emelk_kv_geometry *g, void *k_poo
  * (text/generator/detail.hpp:4297-4372).  head_dim 64 and 128 run on MFMA,
  * f16 and q8_0 pools alike (q8_0 values enter the MFMAs exactly, as two
  * fp16 parts; values of magnitude 65520 or more do not fit), and so does
- * head_dim 256 on f16 pools.  head_dim 512, and 256 on q8_0 pools, run row
- * by row through the decode kernel (n_seq * n_q <= 65535, and a row's
- * context, table_stride * block_tokens tokens at most, must fit 1022
- * pages). */
+ * head_dim 256.  head_dim 512 runs row by row through the decode kernel
+ * (n_seq * n_q <= 65535, and a row's context, table_stride * block_tokens
+ * tokens at most, must fit 1022 pages). */
 emel_error_type emelk_attn_prefill_chunk(const emelk_kv_geometry *g, const void *k_pool,
                                          const void *v_pool, int32_t layer, const float *q,
                                          float *out, int32_t n_seq, int32_t n_q,

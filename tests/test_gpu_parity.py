@@ -687,7 +687,8 @@ Q8_PREFILL_CASES = [
     (16, 2, 64, 8, [19, 0], 40, None),            # G=8, pages of 8
     (8, 2, 128, 32, [100, 37], 40, (0, 1)),       # NaN-filled pool, an invalid page
     (8, 2, 128, 16, [100, 37], 40, (1, 2)),
-    (8, 1, 256, 16, [40], 9, None),               # head_dim 256: row by row
+    (8, 1, 256, 16, [40], 9, None),               # head_dim 256: 4 waves, 32-key tiles
+    (8, 2, 256, 32, [70, 3], 36, (0, 1)),         # head_dim 256, NaN pool, invalid page
 ]
 
 
