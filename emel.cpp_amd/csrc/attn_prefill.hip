@@ -770,9 +770,10 @@ extern "C" emel_error_type emelk_attn_prefill_chunk(const emelk_kv_geometry *g, 
     return EMELK_ERR_INVALID_REQUEST;
   }
   if (L.head_dim == 512) {
-    // head_dim 512 (whose O and Q^T tiles do not fit one wave's registers):
-    // row by row through the decode kernel, as the reference's per-row loop
-    // does
+    // head_dim 512: row by row through the decode kernel, as the reference's
+    // per-row loop does.  One wave's 32 x 512 O tile and Q^T operand take
+    // 384 of its 512 registers; built that way the kernel spills about
+    // 1500 registers per lane.
     return emelk::decode_rows(L, k_pool, v_pool, layer, q, out, n_seq, n_q, q_start,
                               block_tables, table_stride, scale, static_cast<hipStream_t>(stream));
   }
