@@ -335,6 +335,11 @@ struct emelk_kv_cache {
   int32_t *move_slot = nullptr;  // device int32[2] for single-page copies
   int32_t *move_host = nullptr;  // pinned staging for move_slot
   hipStream_t stream = nullptr;
+  // device view upload: pinned snapshot staging (allocated on first use)
+  // and the event that tells when the previous upload has read it
+  emelk_view_snapshot *view_host = nullptr;
+  hipEvent_t view_read = nullptr;
+  bool view_pending = false;
 };
 
 extern "C" emel_error_type emelk_kv_cache_create(const emelk_kv_geometry *g, void *stream,
@@ -368,7 +373,45 @@ extern "C" void emelk_kv_cache_destroy(emelk_kv_cache *c) {
   if (c->v_pool) (void)hipFree(c->v_pool);
   if (c->move_slot) (void)hipFree(c->move_slot);
   if (c->move_host) (void)hipHostFree(c->move_host);
+  if (c->view_host) (void)hipHostFree(c->view_host);
+  if (c->view_read) (void)hipEventDestroy(c->view_read);
   delete c;
+}
+
+// capture_view (kv/sm.hpp:450-465 -> view::snapshot, memory/view.hpp:59-117)
+// delivered to device memory: the actor fills the pinned staging snapshot,
+// which is copied on the cache's stream, so the copy is ordered with the
+// page copies of earlier allocate_slots calls and before later kernels.
+extern "C" emel_error_type emelk_kv_cache_upload_view(emelk_kv_cache *c, emelk_kv_actor *actor,
+                                                      emelk_view_snapshot *view_dev) {
+  if (c == nullptr || actor == nullptr || view_dev == nullptr) return EMELK_ERR_INVALID_REQUEST;
+  if (c->view_host == nullptr) {
+    if (hipHostMalloc(reinterpret_cast<void **>(&c->view_host), sizeof(emelk_view_snapshot),
+                      hipHostMallocDefault) != hipSuccess) {
+      c->view_host = nullptr;
+      return EMELK_ERR_OUT_OF_MEMORY;
+    }
+    if (hipEventCreateWithFlags(&c->view_read, hipEventDisableTiming) != hipSuccess) {
+      c->view_read = nullptr;
+      return EMELK_ERR_BACKEND;
+    }
+  }
+  if (c->view_pending) {  // the copy engine may still read the staging snapshot
+    if (hipEventSynchronize(c->view_read) != hipSuccess) return EMELK_ERR_BACKEND;
+    c->view_pending = false;
+  }
+  int32_t err = EMELK_ERR_NONE;
+  emelk_event_capture_view ev{c->view_host, &err};
+  if (!emelk_kv_capture_view(actor, &ev)) {
+    return err != EMELK_ERR_NONE ? static_cast<emel_error_type>(err) : EMELK_ERR_INTERNAL;
+  }
+  if (hipMemcpyAsync(view_dev, c->view_host, sizeof(emelk_view_snapshot), hipMemcpyHostToDevice,
+                     c->stream) != hipSuccess ||
+      hipEventRecord(c->view_read, c->stream) != hipSuccess) {
+    return EMELK_ERR_BACKEND;
+  }
+  c->view_pending = true;
+  return EMELK_ERR_NONE;
 }
 
 extern "C" void *emelk_kv_cache_k_pool(emelk_kv_cache *c) { return c ? c->k_pool : nullptr; }

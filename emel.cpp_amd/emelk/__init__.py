@@ -247,6 +247,7 @@ _SIGNATURES = [
     ("emelk_kv_cache_stream", _P, [_P]),
     ("emelk_kv_cache_copy_block", ctypes.c_bool,
      [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _P, c_i32p]),
+    ("emelk_kv_cache_upload_view", ctypes.c_uint32, [_P, _P, _P]),
     ("emelk_batch_plan", ctypes.c_bool,
      [ctypes.POINTER(PlanRequest), ctypes.POINTER(PlanResult), ctypes.POINTER(ctypes.c_uint32)]),
     ("emelk_batch_plan_mode", ctypes.c_bool,
@@ -545,6 +546,24 @@ class KvCache:
 
     def v_pool_ptr(self):
         return lib.emelk_kv_cache_v_pool(self.handle)
+
+    def upload_view(self, actor, view_dev):
+        """capture_view into the device buffer view_dev (uint8 tensor of at
+        least ctypes.sizeof(Snapshot) bytes) on the cache's stream."""
+        assert view_dev.numel() * view_dev.element_size() >= ctypes.sizeof(Snapshot)
+        _check(lib.emelk_kv_cache_upload_view(self.handle, actor.handle, _ptr(view_dev)),
+               "emelk_kv_cache_upload_view")
+
+    @staticmethod
+    def view_fields(view_dev, n_seq):
+        """(kv_lens, block_tables) of sequences 0..n_seq-1, as tensors over
+        the device snapshot (no copy)."""
+        lo = Snapshot.sequence_length_values.offset
+        bo = Snapshot.sequence_kv_blocks.offset
+        lens = view_dev[lo:lo + 4 * n_seq].view(dtype=__import__("torch").int32)
+        tables = view_dev[bo:bo + 2 * MAX_BLOCKS_PER_SEQUENCE * n_seq].view(
+            dtype=__import__("torch").int16).view(n_seq, MAX_BLOCKS_PER_SEQUENCE)
+        return lens, tables
 
     def close(self):
         if self.handle and lib is not None:  # lib is None during interpreter teardown

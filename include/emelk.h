@@ -357,6 +357,16 @@ void *emelk_kv_cache_stream(const emelk_kv_cache *cache);
  * one page (all layers, K and V) on the cache's stream. */
 bool emelk_kv_cache_copy_block(int32_t src_block, int32_t dst_block, int32_t block_tokens,
                                void *user_data, int32_t *error_out);
+/* capture_view into device memory (kv/sm.hpp:450-465, memory/view.hpp:59-117):
+ * the actor's snapshot is copied to view_dev (sizeof(emelk_view_snapshot),
+ * 2.1 MB) on the cache's stream, after the page copies already enqueued
+ * there.  Device consumers read it in place: sequence_kv_blocks is a block
+ * table with rows by sequence id and table_stride
+ * EMELK_MAX_BLOCKS_PER_SEQUENCE, and sequence_length_values holds kv_lens,
+ * so sequences 0..n-1 decode straight from the view.  (A decode step that
+ * needs only some rows moves fewer bytes with emelk_kv_export_block_tables.) */
+emel_error_type emelk_kv_cache_upload_view(emelk_kv_cache *cache, emelk_kv_actor *actor,
+                                           emelk_view_snapshot *view_dev);
 
 /* Multi-sequence step executor: the reference generator's per-token flow
  * (allocate_slots with copy_kv_cache_block, text/generator/actions.hpp:460-474;

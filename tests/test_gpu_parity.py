@@ -813,3 +813,39 @@ def test_prefill_chunk_head_dim_512_row_route(device):
     # head_dim 512 takes the row-by-row route through the decode kernel
     banner("prefill chunk at head_dim 512 (row by row)")
     _prefill_case(device, 8, 2, 512, 16, [0, 70], 13, seed=82)
+
+
+def test_decode_straight_from_the_device_view(device):
+    """emelk_kv_cache_upload_view puts the actor's capture_view snapshot in
+    device memory byte for byte; its length values and block rows then serve
+    as kv_lens and block_tables (stride MAX_BLOCKS_PER_SEQUENCE), and decode
+    from them is bit-identical to decode from the exported tables."""
+    import ctypes
+    import torch
+    banner("decode from the device snapshot (capture_view uploaded)")
+    sc = Scenario(n_layer=2, n_head=8, n_kv=2, head_dim=128, block_tokens=32,
+                  lens=[300, 77, 1000], seed=91)
+    cache = emelk.KvCache(sc.g)
+    view_dev = torch.zeros(ctypes.sizeof(emelk.Snapshot), dtype=torch.uint8, device=device)
+    cache.upload_view(sc.actor, view_dev)
+    torch.cuda.synchronize()
+    host = emelk.Snapshot()
+    ok, err = sc.actor.capture_view(host)
+    assert ok and err == 0
+    want = np.frombuffer(bytes(host), dtype=np.uint8)
+    np.testing.assert_array_equal(view_dev.cpu().numpy(), want)
+    lens, tables = emelk.KvCache.view_fields(view_dev, sc.n_seq)
+    rng = np.random.default_rng(92)
+    q = torch.from_numpy(rng.standard_normal((sc.n_seq, 8 * 128)).astype(np.float32)).to(device)
+    ws = torch.empty(emelk.decode_workspace_bytes(sc.g, sc.n_seq, 1000), dtype=torch.uint8,
+                     device=device)
+    a = torch.full_like(q, float("nan"))
+    b = torch.full_like(q, float("nan"))
+    emelk.decode(sc.g, sc.k_pool, sc.v_pool, 1, q, a, lens, 1000, tables, 1 / np.sqrt(128), ws)
+    exp_lens = torch.tensor(sc.lens, dtype=torch.int32, device=device)
+    emelk.decode(sc.g, sc.k_pool, sc.v_pool, 1, q, b, exp_lens, 1000, sc.tables, 1 / np.sqrt(128),
+                 ws)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(a.cpu().numpy(), b.cpu().numpy())
+    assert np.isfinite(a.cpu().numpy()).all()
+    cache.close()
