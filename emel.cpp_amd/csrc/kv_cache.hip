@@ -378,7 +378,7 @@ extern "C" void emelk_kv_cache_destroy(emelk_kv_cache *c) {
   delete c;
 }
 
-// capture_view (kv/sm.hpp:450-465 -> view::snapshot, memory/view.hpp:59-117)
+// capture_view (kv/sm.hpp:448-465 -> view::snapshot, memory/view.hpp:59-117)
 // delivered to device memory: the actor fills the pinned staging snapshot,
 // which is copied on the cache's stream, so the copy is ordered with the
 // page copies of earlier allocate_slots calls and before later kernels.

@@ -357,7 +357,7 @@ void *emelk_kv_cache_stream(const emelk_kv_cache *cache);
  * one page (all layers, K and V) on the cache's stream. */
 bool emelk_kv_cache_copy_block(int32_t src_block, int32_t dst_block, int32_t block_tokens,
                                void *user_data, int32_t *error_out);
-/* capture_view into device memory (kv/sm.hpp:450-465, memory/view.hpp:59-117):
+/* capture_view into device memory (kv/sm.hpp:448-465, memory/view.hpp:59-117):
  * the actor's snapshot is copied to view_dev (sizeof(emelk_view_snapshot),
  * 2.1 MB) on the cache's stream, after the page copies already enqueued
  * there.  Device consumers read it in place: sequence_kv_blocks is a block
