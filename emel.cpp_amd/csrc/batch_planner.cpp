@@ -2,9 +2,9 @@
 //
 // Restates emel::batch::planner (src/emel/batch/planner/): the outer
 // machine validates the request and normalises the step size
-// (sm.hpp:20-60, detail.hpp:129-190, actions.hpp:62-76), then one of three
-// mode machines builds the plan (modes/simple/actions.hpp:33-55,
-// modes/sequential/actions.hpp:30-92, modes/equal/actions.hpp:34-268), and
+// (sm.hpp:20-60, detail.hpp:129-233, actions.hpp:64-75), then one of three
+// mode machines builds the plan (modes/simple/actions.hpp:32-54,
+// modes/sequential/actions.hpp:30-93, modes/equal/actions.hpp:34-269), and
 // a plan counts as complete only when every token was placed
 // (guards.hpp:9-23).  Error bits accumulate as the reference's transitions
 // add them: a failure inside a mode's planning pass is reported together
@@ -34,7 +34,7 @@ struct plan_state {
   uint32_t err = 0;
   int32_t step = 0;  // effective step size
 
-  // Sequence set of token i (detail.hpp:187-233): its mask row when masks
+  // Sequence set of token i (detail.hpp:190-233): its mask row when masks
   // are given, else the bit of its primary id, else sequence 0.
   seq_mask mask_of(int32_t i) const {
     seq_mask m{};
@@ -53,7 +53,7 @@ struct plan_state {
     return m;
   }
 
-  // Plan storage (detail.hpp:278-338).
+  // Plan storage (detail.hpp:297-346).
   void clear() {
     out.step_count = 0;
     out.total_outputs = 0;
@@ -84,7 +84,7 @@ struct plan_state {
     }
   }
 
-  // Outputs of the plan (detail.hpp:257-276): every token, the masked
+  // Outputs of the plan (detail.hpp:279-295): every token, the masked
   // tokens, or the last token only.
   int32_t count_outputs() const {
     if (rq.output_all) return rq.n_tokens;
@@ -176,7 +176,7 @@ uint32_t input_errors(const emelk_plan_request &rq) {
 
 // ---- modes ------------------------------------------------------------
 
-// simple (modes/simple/actions.hpp:33-55): consecutive chunks of `step`.
+// simple (modes/simple/actions.hpp:32-54): consecutive chunks of `step`.
 void plan_simple(plan_state &S) {
   const int32_t n = S.rq.n_tokens;
   for (int32_t start = 0; start < n; start += S.step) {
@@ -188,7 +188,7 @@ void plan_simple(plan_state &S) {
   S.finish_offsets();
 }
 
-// sequential (modes/sequential/actions.hpp:30-92): a step starts at the
+// sequential (modes/sequential/actions.hpp:30-93): a step starts at the
 // first unused token and takes, in order, unused tokens whose sequence set
 // lies inside the set of the token taken before them, up to `step` tokens.
 // Unused tokens are kept in a linked list in token order, so a step's
@@ -229,7 +229,7 @@ void plan_sequential(plan_state &S) {
   S.finish_offsets();
 }
 
-// equal, general path (modes/equal/actions.hpp:34-139): each step picks a
+// equal, general path (modes/equal/actions.hpp:34-145): each step picks a
 // group of pairwise disjoint sequence sets in token order (with
 // equal_sequential and primary ids, each next primary id one above the
 // last; the scan stops once the group has one more member than the step
@@ -308,7 +308,7 @@ void plan_equal_general(plan_state &S) {
   S.finish_offsets();
 }
 
-// equal, primary-id path (modes/equal/actions.hpp:141-268): the same
+// equal, primary-id path (modes/equal/actions.hpp:147-269): the same
 // grouping over primary ids only, with each sequence's tokens listed once
 // in token order.
 void plan_equal_primary(plan_state &S) {
@@ -452,23 +452,23 @@ extern "C" bool emelk_batch_plan(const emelk_plan_request *request, emelk_plan_r
   }
   plan_state S{*request, *result};
   S.clear();
-  // input validation (sm.hpp:27-33): every cause, plus invalid_request
+  // input validation (sm.hpp:28-35): every cause, plus invalid_request
   const uint32_t bad = input_errors(*request);
   if (bad != 0) {
     err = bad | EMELK_PLAN_ERR_INVALID_REQUEST;
     return false;
   }
-  // step size (actions.hpp:62-72): n_steps when positive, within [1, n_tokens]
+  // step size (actions.hpp:64-75): n_steps when positive, within [1, n_tokens]
   const int32_t requested = request->n_steps > 0 ? request->n_steps : request->n_tokens;
   S.step = std::max<int32_t>(1, std::min<int32_t>(requested, request->n_tokens));
   if (request->mode != EMELK_PLAN_SIMPLE && request->mode != EMELK_PLAN_EQUAL &&
       request->mode != EMELK_PLAN_SEQUENTIAL) {
-    err = EMELK_PLAN_ERR_INVALID_MODE | EMELK_PLAN_ERR_INVALID_REQUEST;  // actions.hpp:104-109
+    err = EMELK_PLAN_ERR_INVALID_MODE | EMELK_PLAN_ERR_INVALID_REQUEST;  // actions.hpp:101-106
     return false;
   }
   run_mode(S);
   // a failed mode reports its own bits; an incomplete plan without any
-  // is an internal error (actions.hpp:116-119)
+  // is an internal error (actions.hpp:113-116)
   err = S.err != 0 ? S.err : (S.complete() ? 0u : EMELK_PLAN_ERR_INTERNAL_ERROR);
   return err == 0;
 }

@@ -622,7 +622,7 @@ class DevPtr:
 
 
 class BatchPlan:
-    """The batch planner's process_event (src/emel/batch/planner/sm.hpp:128-134)
+    """The batch planner's process_event (src/emel/batch/planner/sm.hpp:130-136)
     on host arrays: ``BatchPlan(token_ids, n_steps, mode, ...)`` runs it and
     keeps ``accepted``, ``error`` (planner error bits), ``step_sizes``,
     ``steps`` (the token indices of each step), ``total_outputs`` and

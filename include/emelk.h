@@ -423,7 +423,7 @@ typedef enum emelk_plan_mode {
   EMELK_PLAN_SEQUENTIAL = 2
 } emelk_plan_mode;
 
-/* Planner error bits (batch/planner/errors.hpp:6-24). */
+/* Planner error bits (batch/planner/errors.hpp:6-25). */
 #define EMELK_PLAN_ERR_INVALID_REQUEST (1u << 0)
 #define EMELK_PLAN_ERR_INVALID_TOKEN_DATA (1u << 1)
 #define EMELK_PLAN_ERR_INVALID_STEP_SIZE (1u << 2)
@@ -439,7 +439,7 @@ typedef enum emelk_plan_mode {
 #define EMELK_PLAN_ERR_ALGORITHM_FAILED (1u << 13)
 #define EMELK_PLAN_ERR_INTERNAL_ERROR (1u << 15)
 
-/* event::plan_request (batch/planner/events.hpp:20-41) without the
+/* event::plan_request (batch/planner/events.hpp:24-42) without the
  * callbacks.  seq_masks: n_tokens rows of seq_mask_words uint64 words (bit s
  * = sequence s); seq_primary_ids: one sequence id per token; with neither,
  * every token is on sequence 0.  The reference's default seq_mask_words is
@@ -460,7 +460,7 @@ typedef struct emelk_plan_request {
   int32_t output_all;
 } emelk_plan_request;
 
-/* events::plan_done (events.hpp:62-71): step s holds the token indices
+/* events::plan_done (events.hpp:64-73): step s holds the token indices
  * step_token_indices[step_token_offsets[s] .. step_token_offsets[s+1]) and
  * has step_sizes[s] of them.  Counts are zero after a refused request. */
 typedef struct emelk_plan_result {
@@ -474,7 +474,7 @@ typedef struct emelk_plan_result {
 
 /* The planner's process_event: true iff a plan was produced; *error_out
  * (optional) receives the error bits (0 on success).  Replaces
- * Planner::process_event (batch/planner/sm.hpp:128-134). */
+ * Planner::process_event (batch/planner/sm.hpp:130-136). */
 bool emelk_batch_plan(const emelk_plan_request *request, emelk_plan_result *result,
                       uint32_t *error_out);
 /* One mode's planner with the step size given (modes::*::sm with

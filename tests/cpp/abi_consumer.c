@@ -2,7 +2,7 @@
  * header compiles as C, and the host entry points work from C the way the
  * reference's hybrid memory facade drives a kv_binding (every event through
  * the dispatch table, src/emel/memory/hybrid/actions.hpp:199-213) and the
- * way its generator plans a prompt (text/generator/actions.hpp:208-241).
+ * way its generator plans a prompt (text/generator/actions.hpp:209-242).
  * No device calls: it runs on a machine without a GPU.  Built and run by
  * tests/test_abi.py. */
 #include <stdio.h>

@@ -280,7 +280,7 @@ def test_step_sequences_rejects_mixed_steps():
 
 
 # ---- the bucketed / linked-list passes against the step rules written out
-# token by token (modes/sequential/actions.hpp:30-92, modes/equal/
+# token by token (modes/sequential/actions.hpp:30-93, modes/equal/
 # actions.hpp:34-139), on seeded batches with multi-sequence masks ----------
 
 def _sequential_rules(masks, step):
