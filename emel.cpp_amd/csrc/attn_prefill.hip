@@ -677,7 +677,8 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
   // V buffers, 228 VGPRs): 812 vs 826 TFLOP/s, and 790 with the K reads and
   // MFMAs explicitly interleaved into the softmax (sched_group_barrier).
   // Q^T kept in LDS instead of registers (225 instead of 256 VGPRs, one
-  // more LDS operand read per k-step): 801 vs 834 TFLOP/s.
+  // more LDS operand read per k-step): 801 vs 834 TFLOP/s.  Four waves of
+  // 32 rows (the head_dim 256 layout) at head_dim 128: 490 vs 810.
   stage_t R;
   load_tile(0, R);
   store_tile(0, 0, R);
