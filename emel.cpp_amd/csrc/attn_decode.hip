@@ -54,6 +54,8 @@ constexpr int k_decode_nb = 2;
 // with 3 or 4 tile sets in flight; the shuffles that sum the blocks and hand
 // P to the V lanes lengthen each tile's dependent chain.  Scaling K to fp16
 // before the MFMA instead breaks the 2e-3 bar on the x20-outlier data.
+// Workgroups of 4 KV heads instead of 8 ran at 4.44 vs 5.51 TB/s there, and
+// with 3 waves per SIMD (168 VGPRs, one tile set in flight) at 3.06.
 
 // Waves per workgroup = KV heads per workgroup: min(n_head_kv, 8) when it
 // divides n_head_kv, else 1.
