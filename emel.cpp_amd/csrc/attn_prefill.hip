@@ -774,7 +774,8 @@ extern "C" emel_error_type emelk_attn_prefill_chunk(const emelk_kv_geometry *g, 
     // head_dim 512: row by row through the decode kernel, as the reference's
     // per-row loop does.  One wave's 32 x 512 O tile and Q^T operand take
     // 384 of its 512 registers; built that way the kernel spills about
-    // 1500 registers per lane.
+    // 1500 registers per lane, and with wave pairs that split O's columns
+    // (each still holding the 128-register Q^T operand) about 350.
     return emelk::decode_rows(L, k_pool, v_pool, layer, q, out, n_seq, n_q, q_start,
                               block_tables, table_stride, scale, static_cast<hipStream_t>(stream));
   }
