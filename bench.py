@@ -45,6 +45,8 @@ PMC_TRAFFIC_BYTES = {
     "llama3-8b-q8_0-b32-ctx16k": 1155282739,
     "llama3-8b-prefill512-evict25": 285551820,
     "llama3-8b-q8_0-prefill512-evict25": 214867558,
+    "gemma4-d256-prefill512-evict25": 105300848,
+    "gemma4-d256-q8_0-prefill512-evict25": 87748528,
 }
 
 CONFIGS = {
