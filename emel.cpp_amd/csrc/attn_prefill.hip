@@ -678,7 +678,10 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
   // MFMAs explicitly interleaved into the softmax (sched_group_barrier).
   // Q^T kept in LDS instead of registers (225 instead of 256 VGPRs, one
   // more LDS operand read per k-step): 801 vs 834 TFLOP/s.  Four waves of
-  // 32 rows (the head_dim 256 layout) at head_dim 128: 490 vs 810.
+  // 32 rows (the head_dim 256 layout) at head_dim 128: 490 vs 810.  At
+  // head_dim 256 (one wave per SIMD), the next tile's scores computed in
+  // the same stretch as this tile's softmax, K and V staged two tiles ahead
+  // in rings of 3: 458-463 vs 488 TFLOP/s.
   stage_t R;
   load_tile(0, R);
   store_tile(0, 0, R);
