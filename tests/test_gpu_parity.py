@@ -849,3 +849,37 @@ def test_decode_straight_from_the_device_view(device):
     np.testing.assert_array_equal(a.cpu().numpy(), b.cpu().numpy())
     assert np.isfinite(a.cpu().numpy()).all()
     cache.close()
+
+
+@pytest.mark.parametrize("kv_type", [emelk.KV_F16, emelk.KV_Q8_0])
+def test_prefill_config5_full_size_sampled_rows(device, kv_type):
+    """The config-5 chunk at its full size: 8 sequences x (4096 cached + 512
+    new rows), Llama-3-8B heads, 32-token pages on a seeded permutation.
+    One layer runs on the GPU, and 24 seeded (sequence, row) samples, first
+    and last rows included, are checked against the oracle's per-row route."""
+    import torch
+    banner(f"prefill chunk at the full config-5 size, kv_type={kv_type}")
+    P0, NQ, B = 4096, 512, 8
+    sc = Scenario(n_layer=1, n_head=32, n_kv=8, head_dim=128, block_tokens=32,
+                  lens=[P0 + NQ] * B, seed=101, kv_type=kv_type,
+                  outlier_frac=0.01 if kv_type == emelk.KV_Q8_0 else 0.0)
+    rng = np.random.default_rng(102)
+    q = rng.standard_normal((B, NQ, 32, 128)).astype(np.float32)
+    qd = torch.from_numpy(q).to(device)
+    out = torch.full_like(qd, float("nan"))
+    qs = torch.full((B,), P0, dtype=torch.int32, device=device)
+    scale = 1.0 / np.sqrt(128)
+    emelk.prefill_chunk(sc.g, sc.k_pool, sc.v_pool, 0, qd, out, qs, sc.tables, scale)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert np.isfinite(got).all()
+    kc, vc = sc.oracle_cache(0)
+    route = oracle.compute_attention_f16 if kv_type == emelk.KV_F16 else \
+        oracle.compute_attention_q8_0
+    samples = [(0, 0), (B - 1, NQ - 1)] + [(int(rng.integers(B)), int(rng.integers(NQ)))
+                                           for _ in range(22)]
+    for s, r in samples:
+        limit = P0 + r + 1
+        want = route(q[s, r].ravel(), kc, vc, sc.tables_host[s], 32, 32, 8, 128, limit, limit,
+                     scale)
+        assert_close(got[s, r].ravel(), want, what=f"seq {s} row {r}")
