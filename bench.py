@@ -293,6 +293,46 @@ def main():
                          f"extrapolated x{L} layers; oracle restatement of compute_attention, "
                          f"{nthreads} threads",
                "steps_per_s": round(1.0 / cpu_step_s, 5)}
+    elif not args.no_cpu_baseline:
+        # q8_0: the oracle's q8_0 route (dequantize_row_q8_0 values, the
+        # same softmax and fp16 probabilities as the f16 route) on a seeded
+        # sample of sequences of layer 0, one thread
+        import oracle
+        layer = 0
+        lb = pool_bytes // L
+        def token_major(pool):
+            # pool [page][kv_head] regions of (values [bt][D], scales
+            # [bt][D/32]) -> reference token-major BLOCK_Q8_0 rows
+            raw = pool[layer * lb:(layer + 1) * lb].cpu().numpy().reshape(max_blocks, HK, -1)
+            qs = raw[:, :, :BT * D].view(np.int8).reshape(max_blocks, HK, BT, D // 32, 32)
+            ds = raw[:, :, BT * D:].view(np.uint16).reshape(max_blocks, HK, BT, D // 32)
+            out_c = np.empty((max_blocks, BT, HK, D // 32), oracle.BLOCK_Q8_0)
+            out_c["qs"] = qs.transpose(0, 2, 1, 3, 4)
+            out_c["d"] = ds.transpose(0, 2, 1, 3)
+            return out_c.reshape(max_blocks * BT, HK * D // 32)
+        kc, vc = token_major(k_pool), token_major(v_pool)
+        pick = sorted(np.random.default_rng(args.seed + 1).choice(B, size=min(4, B),
+                                                                  replace=False).tolist())
+        qh = q[layer].view(B, H * D).cpu().numpy()
+        got = out[layer].view(B, H * D).cpu().numpy()
+        errs, t_cpu = [], 0.0
+        for s in pick:
+            t1 = time.perf_counter()
+            want = oracle.compute_attention_q8_0(qh[s], kc, vc, tables_h[s], BT, H, HK, D,
+                                                 int(lens[s]), int(lens[s]), scale)
+            t_cpu += time.perf_counter() - t1
+            errs.append((np.abs(got[s].astype(np.float64) - want),
+                         2e-3 + 1e-2 * np.abs(want.astype(np.float64))))
+        parity = {"layer": layer, "sequences": pick,
+                  "max_abs_err": float(max(e.max() for e, _ in errs)),
+                  "within_tolerance": bool(all(np.all(e <= tol) for e, tol in errs))}
+        cpu_step_s = t_cpu / len(pick) * B * L
+        cpu = {"value": round(step_kv_bytes / cpu_step_s / 1e9, 4), "unit": "GB/s", "cores": 1,
+               "kind": "port",
+               "sample": f"{len(pick)} sequences x 1 layer of the step ({t_cpu:.2f}s), "
+                         f"extrapolated to {B} sequences x {L} layers; oracle q8_0 route, "
+                         "1 thread",
+               "steps_per_s": round(1.0 / cpu_step_s, 6)}
 
     result = {
         "metric": "KV-read HBM GB/s (% of peak) + decode steps/s, 8B-shape b64 ctx8k",
