@@ -299,18 +299,8 @@ def main():
         # sample of sequences of layer 0, one thread
         import oracle
         layer = 0
-        lb = pool_bytes // L
-        def token_major(pool):
-            # pool [page][kv_head] regions of (values [bt][D], scales
-            # [bt][D/32]) -> reference token-major BLOCK_Q8_0 rows
-            raw = pool[layer * lb:(layer + 1) * lb].cpu().numpy().reshape(max_blocks, HK, -1)
-            qs = raw[:, :, :BT * D].view(np.int8).reshape(max_blocks, HK, BT, D // 32, 32)
-            ds = raw[:, :, BT * D:].view(np.uint16).reshape(max_blocks, HK, BT, D // 32)
-            out_c = np.empty((max_blocks, BT, HK, D // 32), oracle.BLOCK_Q8_0)
-            out_c["qs"] = qs.transpose(0, 2, 1, 3, 4)
-            out_c["d"] = ds.transpose(0, 2, 1, 3)
-            return out_c.reshape(max_blocks * BT, HK * D // 32)
-        kc, vc = token_major(k_pool), token_major(v_pool)
+        kc, vc = (pool_token_major(p_, layer, L, max_blocks, HK, BT, D, True, oracle)
+                  for p_ in (k_pool, v_pool))
         pick = sorted(np.random.default_rng(args.seed + 1).choice(B, size=min(4, B),
                                                                   replace=False).tolist())
         qh = q[layer].view(B, H * D).cpu().numpy()
@@ -368,6 +358,24 @@ def main():
         "parity_full_size": parity,
     }
     print(json.dumps(result), flush=True)
+
+
+def pool_token_major(pool, layer, n_layer, max_blocks, n_kv, bt, d, q8, oracle):
+    """One layer of a device pool in the reference's token-major paged
+    layout (key_cache[phys][kv_dim], text/generator/detail.hpp:2984-3005):
+    uint16 halves for f16 pools, BLOCK_Q8_0 rows for q8_0 pools (whose
+    regions hold values [bt][d] then scales [bt][d/32])."""
+    lb = pool.numel() // n_layer
+    raw = pool[layer * lb:(layer + 1) * lb].cpu().numpy().reshape(max_blocks, n_kv, -1)
+    if not q8:
+        h = raw.view(np.uint16).reshape(max_blocks, n_kv, bt, d)
+        return np.ascontiguousarray(h.transpose(0, 2, 1, 3)).reshape(max_blocks * bt, n_kv * d)
+    qs = raw[:, :, :bt * d].view(np.int8).reshape(max_blocks, n_kv, bt, d // 32, 32)
+    ds = raw[:, :, bt * d:].view(np.uint16).reshape(max_blocks, n_kv, bt, d // 32)
+    out = np.empty((max_blocks, bt, n_kv, d // 32), oracle.BLOCK_Q8_0)
+    out["qs"] = qs.transpose(0, 2, 1, 3, 4)
+    out["d"] = ds.transpose(0, 2, 1, 3)
+    return out.reshape(max_blocks * bt, n_kv * d // 32)
 
 
 def prefill_evict(args, torch, emelk, dev):
@@ -457,6 +465,41 @@ def prefill_evict(args, torch, emelk, dev):
     flops_layer = 4.0 * D * H * B * float(np.sum(P0 + rows + 1))
     tflops = flops_layer / (attn_ms * 1e-3) / 1e12
 
+    # parity sample + CPU baseline: the last layer's output (out is reused
+    # per layer) for 4 seeded (sequence, row) pairs against the oracle's
+    # per-row route (text/generator/detail.hpp:4297-4372), one thread
+    parity = cpu = None
+    if not args.no_cpu_baseline:
+        import oracle
+        layer = L - 1
+        kc, vc = (pool_token_major(p_, layer, L, max_blocks, HK, BT, D, q8, oracle)
+                  for p_ in (k_pool, v_pool))
+        tables_h = tables.cpu().numpy().view(np.uint16)
+        route = oracle.compute_attention_q8_0 if q8 else oracle.compute_attention_f16
+        prng = np.random.default_rng(args.seed + 2)
+        pick = [(int(prng.integers(B)), int(prng.integers(NQ))) for _ in range(4)]
+        qh = q[layer].cpu().numpy()
+        got = out.cpu().numpy()
+        worst, ok_all, t_cpu, keys = 0.0, True, 0.0, 0
+        for s_, r_ in pick:
+            lim = P0 + r_ + 1
+            t1 = time.perf_counter()
+            want = route(qh[s_, r_].ravel(), kc, vc, tables_h[s_], BT, H, HK, D, lim, lim, scale)
+            t_cpu += time.perf_counter() - t1
+            keys += lim
+            e = np.abs(got[s_, r_].ravel().astype(np.float64) - want)
+            worst = max(worst, float(e.max()))
+            ok_all = ok_all and bool(np.all(e <= 2e-3 + 1e-2 * np.abs(want)))
+        parity = {"layer": layer, "rows": pick, "max_abs_err": worst, "within_tolerance": ok_all}
+        # the per-row route's time per attended key, scaled to a layer's keys
+        layer_keys = B * float(np.sum(P0 + rows + 1))
+        cpu_layer_s = t_cpu / keys * layer_keys
+        cpu = {"value": round(flops_layer / cpu_layer_s / 1e12, 6), "unit": "TFLOP/s", "cores": 1,
+               "kind": "port",
+               "sample": f"{len(pick)} rows of layer {layer} ({t_cpu:.2f}s), scaled by attended "
+                         "keys to the layer's 4096 rows; oracle per-row route, 1 thread"}
+        del kc, vc
+
     # eviction + compaction
     evicted = 0
     for s in range(B):
@@ -489,6 +532,8 @@ def prefill_evict(args, torch, emelk, dev):
                      "algorithmic_bytes": prefill_bytes,
                      "kernel": "prefill_kernel (HIP events per layer call)",
                      "flops_per_launch": flops_layer, "avg_launch_ms": round(attn_ms, 4)},
+        "cpu_baseline": cpu,
+        "parity_sample": parity,
         "compaction": {"pages_evicted": evicted, "moves": len(moves), "ms": round(copy_ms, 4),
                        "GB/s": round(copy_bytes / (copy_ms * 1e-3) / 1e9, 1),
                        "bytes": copy_bytes},
