@@ -52,6 +52,7 @@ struct emelk_batch_decoder {
   int32_t n_tokens = 0;
   int32_t step_max_kv = 0;
   bool step_open = false;
+  bool fixed_plan = false;  // plan attention for max_kv_len, not the step's longest
 };
 
 namespace {
@@ -209,10 +210,16 @@ extern "C" emel_error_type emelk_batch_decoder_layer(emelk_batch_decoder *d, int
       d->d_tables, d->stride, d->rope, q_norm, k_norm, v_rms, rms_epsilon, d->stream);
   if (e != EMELK_ERR_NONE) return e;
   if (d->n_tokens == 1) {
-    return emelk_attn_decode(&d->g, kp, vp, layer, q_roped, out, d->n_seq, d->d_kv_len,
-                             d->step_max_kv, d->d_tables, d->stride, scale, d->d_ws, d->ws_bytes,
-                             d->stream);
+    const int32_t plan_len = d->fixed_plan ? d->max_kv_len : d->step_max_kv;
+    return emelk_attn_decode(&d->g, kp, vp, layer, q_roped, out, d->n_seq, d->d_kv_len, plan_len,
+                             d->d_tables, d->stride, scale, d->d_ws, d->ws_bytes, d->stream);
   }
   return emelk_attn_prefill_chunk(&d->g, kp, vp, layer, q_roped, out, d->n_seq, d->n_tokens,
                                   d->d_pos, d->d_tables, d->stride, scale, d->stream);
+}
+
+extern "C" emel_error_type emelk_batch_decoder_set_fixed_plan(emelk_batch_decoder *d, int32_t on) {
+  if (d == nullptr) return EMELK_ERR_INVALID_REQUEST;
+  d->fixed_plan = on != 0;
+  return EMELK_ERR_NONE;
 }

@@ -236,6 +236,7 @@ _SIGNATURES = [
     ("emelk_batch_decoder_destroy", None, [_P]),
     ("emelk_batch_decoder_begin_step", ctypes.c_uint32,
      [_P, c_i32p, ctypes.c_int32, ctypes.c_int32, c_i32p]),
+    ("emelk_batch_decoder_set_fixed_plan", ctypes.c_uint32, [_P, ctypes.c_int32]),
     ("emelk_batch_decoder_layer", ctypes.c_uint32,
      [_P, ctypes.c_int32, _P, _P, _P, _P, _P, _P, ctypes.c_int32, ctypes.c_float, ctypes.c_float,
       _P]),
@@ -594,6 +595,11 @@ class BatchDecoder:
         _check(lib.emelk_batch_decoder_begin_step(self.handle, ids, len(seq_ids), n_tokens, pos),
                "emelk_batch_decoder_begin_step")
         return list(pos)
+
+    def set_fixed_plan(self, on=True):
+        """Graph-stable launches (emelk_batch_decoder_set_fixed_plan)."""
+        _check(lib.emelk_batch_decoder_set_fixed_plan(self.handle, int(bool(on))),
+               "emelk_batch_decoder_set_fixed_plan")
 
     def layer(self, layer, q_in, q_roped, k_rows, v_rows, out, scale, q_norm=None, k_norm=None,
               v_rms=False, eps=1e-6):

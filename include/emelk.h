@@ -398,6 +398,15 @@ emel_error_type emelk_batch_decoder_begin_step(emelk_batch_decoder *decoder,
  * n_tokens == 1, emelk_attn_prefill_chunk otherwise).  q_in/q_roped/out:
  * [n_seq][n_tokens][n_head][head_dim] fp32 (q_roped may alias q_in);
  * k_rows/v_rows: [n_seq][n_tokens][n_head_kv][head_dim] fp32. */
+/* Graph-stable launches (no counterpart in the reference, whose generator
+ * runs on the CPU): when on, each layer's attention is planned for the
+ * decoder's max_kv_len instead of the step's longest sequence, so a layer
+ * call's launches depend only on n_seq and n_tokens.  A captured graph of
+ * the layer calls then stays valid for later steps of the same shape
+ * (begin_step runs outside the graph and refreshes the device tables,
+ * positions and lengths the kernels read).  Off by default: the step's own
+ * length gives better split sizes while contexts are short. */
+emel_error_type emelk_batch_decoder_set_fixed_plan(emelk_batch_decoder *decoder, int32_t on);
 emel_error_type emelk_batch_decoder_layer(emelk_batch_decoder *decoder, int32_t layer,
                                           const float *q_in, float *q_roped, const float *k_rows,
                                           const float *v_rows, const float *q_norm,

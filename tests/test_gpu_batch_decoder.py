@@ -215,3 +215,99 @@ def test_batch_decoder_runs_an_equal_plan(device, kv_type):
     # the plan mixes multi-sequence prefill steps with steps of other shapes
     assert any(len(sq) == 3 for sq, _ in shapes) and any(p > 1 for _, p in shapes)
     dec.close()
+
+
+def test_batch_decoder_decode_layers_replay_as_a_graph(device):
+    """With graph-stable launches, one decode step's layer calls are captured
+    in a HIP graph once and replayed for later steps: begin_step refreshes
+    the device tables, positions and lengths outside the graph.  Every
+    replay is checked against the oracle's per-token flow, with host work
+    and synchronisation between replays."""
+    import torch
+    banner("batch decoder: decode layers captured once, replayed over steps")
+    rng = np.random.default_rng(21)
+    g = emelk.geometry(L, H, HKV, D, BT, 64, emelk.KV_F16)
+    actor = emelk.KvActor()
+    assert actor.reserve(4, 64, BT)[0]
+    actor.set_free_order(rng.permutation(64).astype(np.uint16))
+    ids = [0, 1, 2]
+    for s in ids:
+        assert actor.allocate_sequence(s)[0]
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        cache = emelk.KvCache(g, stream=side.cuda_stream)
+        rope = emelk.RopeTable(D, D, 256, BASE, emelk.NEOX_PAIRING, stream=side.cuda_stream)
+        dec = emelk.BatchDecoder(g, actor, cache, rope, max_batch=3, max_kv_len=200,
+                                 stream=side.cuda_stream)
+        dec.set_fixed_plan(True)
+        model = Model()
+        for s in ids:
+            model.ensure(s)
+        n = len(ids)
+        # static buffers the graph reads and writes
+        qb = torch.zeros((L, n, 1, H * D), device=device)
+        kb = torch.zeros((L, n, 1, HKV * D), device=device)
+        vb = torch.zeros((L, n, 1, HKV * D), device=device)
+        qr = torch.zeros_like(qb)
+        ob = torch.zeros_like(qb)
+
+        def fill(step_rows):
+            for layer in range(L):
+                q, k, v = step_rows[layer]
+                qb[layer].copy_(torch.from_numpy(q).view(n, 1, -1))
+                kb[layer].copy_(torch.from_numpy(k).view(n, 1, -1))
+                vb[layer].copy_(torch.from_numpy(v).view(n, 1, -1))
+
+        def layers():
+            for layer in range(L):
+                dec.layer(layer, qb[layer], qr[layer], kb[layer], vb[layer], ob[layer], SCALE)
+
+        def rows():
+            return [(rng.standard_normal((n, H * D)).astype(np.float32),
+                     rng.standard_normal((n, HKV * D)).astype(np.float32),
+                     rng.standard_normal((n, HKV * D)).astype(np.float32)) for _ in range(L)]
+
+        def check(step_rows, pos, what):
+            side.synchronize()
+            got = ob.cpu().numpy()
+            for layer in range(L):
+                q, k, v = step_rows[layer]
+                for i, s in enumerate(ids):
+                    want = model.token(s, layer, q[i], k[i], v[i], pos[i], None, None)
+                    assert_close(got[layer, i, 0], want, what=f"{what} layer {layer} seq {s}")
+
+        # a prompt of 30 tokens per sequence, eager
+        pos = dec.begin_step(ids, 30)
+        for layer in range(L):
+            q = rng.standard_normal((n, 30, H * D)).astype(np.float32)
+            k = rng.standard_normal((n, 30, HKV * D)).astype(np.float32)
+            v = rng.standard_normal((n, 30, HKV * D)).astype(np.float32)
+            out = torch.empty((n, 30, H * D), device=device)
+            qd = torch.from_numpy(q).to(device)
+            dec.layer(layer, qd, qd, torch.from_numpy(k).to(device), torch.from_numpy(v).to(device),
+                      out, SCALE)
+            for i, s in enumerate(ids):
+                for t in range(30):
+                    model.token(s, layer, q[i, t], k[i, t], v[i, t], pos[i] + t, None, None)
+        side.synchronize()
+        # step 1 eager (with the fixed plan), then capture step 2's layers
+        r = rows()
+        fill(r)
+        pos = dec.begin_step(ids, 1)
+        layers()
+        check(r, pos, "eager step")
+        r = rows()
+        fill(r)
+        pos = dec.begin_step(ids, 1)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            layers()
+        graph.replay()
+        check(r, pos, "first replay")
+        for step in range(3):
+            r = rows()
+            fill(r)
+            pos = dec.begin_step(ids, 1)
+            graph.replay()
+            check(r, pos, f"replay {step + 2}")
+        dec.close()
