@@ -72,6 +72,7 @@ def main():
                                                "llama3-8b-q8_0-prefill512-evict25",
                                                "gemma4-d256-prefill512-evict25",
                                                "gemma4-d256-q8_0-prefill512-evict25",
+                                               "gemma4-d512-prefill512-evict25",
                                                "llama3-8b-b64-ctx8k-generator"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--separate-append", action="store_true",
@@ -104,7 +105,8 @@ def main():
     import emelk
 
     if args.config in ("llama3-8b-prefill512-evict25", "llama3-8b-q8_0-prefill512-evict25",
-                       "gemma4-d256-prefill512-evict25", "gemma4-d256-q8_0-prefill512-evict25"):
+                       "gemma4-d256-prefill512-evict25", "gemma4-d256-q8_0-prefill512-evict25",
+                       "gemma4-d512-prefill512-evict25"):
         return prefill_evict(args, torch, emelk, dev)
     if args.config == "llama3-8b-b64-ctx8k-generator":
         return generator(args, torch, emelk, dev)
@@ -391,6 +393,9 @@ def prefill_evict(args, torch, emelk, dev):
         # Gemma-4's sliding-window attention layers: 8 query heads on one KV
         # head of 256 (src/emel/model/gemma4/detail.cpp:24-29); 8 layers
         L, H, HK, D = 8, 8, 1, 256
+    elif args.config.startswith("gemma4-d512"):
+        # its global layers: key length 512 (row-by-row route); 8 layers
+        L, H, HK, D = 8, 8, 1, 512
     q8 = "q8_0" in args.config
     rng = np.random.default_rng(args.seed)
     total = P0 + NQ
