@@ -106,12 +106,26 @@ __device__ __forceinline__ int key_slot(int k) {
   return s * 16 + h * 8 + i;
 }
 
-template <int D, int G_WG, int RB, int KT, bool Q8>
+// Slot of key k (0..31) for the 16-row layout (v_mfma_f32_16x16x32_f16):
+// the score accumulators of a lane group g = lane/16 hold keys 4g..4g+3 and
+// 16+4g..16+4g+3 of its query row, which are P operand k-indices 8g..8g+7.
+__device__ __forceinline__ int key_slot16(int k) {
+  return 8 * ((k & 15) >> 2) + (k >= 16 ? 4 : 0) + (k & 3);
+}
+
+typedef float float4_v __attribute__((ext_vector_type(4)));
+
+template <int D, int G_WG, int RB, int KT, bool Q8, bool M16 = false>
 __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_params P) {
   constexpr int WAVES = G_WG * RB;
   constexpr int NT = WAVES * k_wave;
   constexpr int KSTEPS = D / 16;   // MFMA k-steps for S^T
   constexpr int DCH = D / 32;      // 32-wide dim chunks of O
+  // M16: 16 query rows per wave on v_mfma_f32_16x16x32_f16 (head_dim 512,
+  // whose 32-row O tile and Q^T operand do not fit one wave's registers)
+  constexpr int ROWS = M16 ? 16 : 32;
+  constexpr int KS16 = D / 32;     // M16: k-steps of 32 dims
+  constexpr int OT16 = D / 16;     // M16: 16-column tiles of O
   constexpr int KROW = D + 8;      // padded LDS row (halves) of K
   constexpr int NS = KT / k_sub;   // score sub-tiles per key tile
   constexpr int VROW = KT + 8;     // padded LDS row (halves) of V^T
@@ -135,7 +149,7 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
   // ids are spread over the 8 XCDs; the mapping gives each XCD a contiguous
   // run of (head group, sequence) units with all their query tiles, so the
   // tiles that re-read one unit's K/V share that XCD's L2.
-  const int n_qt = (P.n_q + RB * 32 - 1) / (RB * 32);
+  const int n_qt = (P.n_q + RB * ROWS - 1) / (RB * ROWS);
   const int n_hg = P.L.n_head / G_WG;
   const int total_wg = gridDim.x;
   int lin = blockIdx.x;
@@ -153,21 +167,40 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
   const int head0 = hg * G_WG;
   const int kvh = head0 / group;
   const int head = head0 + wave % G_WG;
-  const int row0 = (qt * RB + wave / G_WG) * 32;
+  const int row0 = (qt * RB + wave / G_WG) * ROWS;
+  const int c16 = lane % 16;  // M16: the lane's query row (and O column) in its block
+  const int g16 = lane / 16;  // M16: lane group
   const int n_q = P.n_q;
   const int q0 = P.q_start[seq];
   const int total = q0 + n_q;
-  const int wg_row_end = min(n_q, (qt + 1) * RB * 32);
+  const int wg_row_end = min(n_q, (qt + 1) * RB * ROWS);
   const int key_end = q0 + wg_row_end;  // exclusive
   const int n_tiles = (key_end + KT - 1) / KT;
-  const int my_row = row0 + l32;
+  const int my_row = row0 + (M16 ? c16 : l32);
   const bool row_ok = my_row < n_q;
   const int my_pos = q0 + my_row;
-  const int wg_first_pos = q0 + qt * RB * 32;  // smallest query position in the WG
+  const int wg_first_pos = q0 + qt * RB * ROWS;  // smallest query position in the WG
 
-  // Q^T operand (B): lane holds query my_row, dims 16*kk + 8*h .. +7.
-  half8_v qop[KSTEPS];
-  {
+  // Q^T operand (B): lane holds query my_row, dims 16*kk + 8*h .. +7
+  // (M16: dims 32*kk + 8*g16 .. +7).
+  half8_v qop[M16 ? 1 : KSTEPS];
+  half8_v qop16[M16 ? KS16 : 1];
+  if constexpr (M16) {
+    const float *qp = P.q + ((static_cast<uint64_t>(seq) * n_q + (row_ok ? my_row : 0)) *
+                                 P.L.n_head + head) * D;
+#pragma unroll
+    for (int kk = 0; kk < KS16; ++kk) {
+      const float4_t a = *reinterpret_cast<const float4_t *>(qp + 32 * kk + 8 * g16);
+      const float4_t b = *reinterpret_cast<const float4_t *>(qp + 32 * kk + 8 * g16 + 4);
+      half8_v v;
+      v[0] = static_cast<half_t>(a.x); v[1] = static_cast<half_t>(a.y);
+      v[2] = static_cast<half_t>(a.z); v[3] = static_cast<half_t>(a.w);
+      v[4] = static_cast<half_t>(b.x); v[5] = static_cast<half_t>(b.y);
+      v[6] = static_cast<half_t>(b.z); v[7] = static_cast<half_t>(b.w);
+      if (!row_ok) v = half8_v{0, 0, 0, 0, 0, 0, 0, 0};
+      qop16[kk] = v;
+    }
+  } else {
     const float *qp = P.q + ((static_cast<uint64_t>(seq) * n_q + (row_ok ? my_row : 0)) *
                                  P.L.n_head + head) * D;
 #pragma unroll
@@ -184,12 +217,15 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
     }
   }
 
-  float16_v o[DCH];
+  float16_v o[M16 ? 1 : DCH];
+  float4_v o16[M16 ? OT16 : 1];
 #pragma unroll
-  for (int c = 0; c < DCH; ++c) {
+  for (int c = 0; c < (M16 ? 1 : DCH); ++c) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[c][r] = 0.0f;
   }
+#pragma unroll
+  for (int c = 0; c < (M16 ? OT16 : 1); ++c) o16[c] = float4_v{0.0f, 0.0f, 0.0f, 0.0f};
   float m = -INFINITY;  // raw-score reference max of this lane's row
   float l = 0.0f;
   const float rescale_raw = k_rescale / P.c;
@@ -445,7 +481,8 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
       if (VITEMS % NT == 0 || item < VITEMS) {
         const int dp = item % (D / 2);
         const int key4 = 4 * (item / (D / 2));  // 4 consecutive keys -> 4 slots
-        const int slot = (key4 / k_sub) * k_sub + key_slot(key4 % k_sub);
+        const int slot = (key4 / k_sub) * k_sub + (M16 ? key_slot16(key4 % k_sub)
+                                                        : key_slot(key4 % k_sub));
         // lanes 8..15 of each 16 write their odd row first: the two rows of
         // a lane are 4 banks apart, so each write instruction spreads over
         // twice as many banks (measured: LDS bank-conflict cycles 13.5M ->
@@ -682,6 +719,111 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
   // head_dim 256 (one wave per SIMD), the next tile's scores computed in
   // the same stretch as this tile's softmax, K and V staged two tiles ahead
   // in rings of 3: 458-463 vs 488 TFLOP/s.
+  // ---- M16 (16 rows per wave, v_mfma_f32_16x16x32_f16) ----
+  // S^T tile j (16 keys) = K (16 x D) . Q^T (D x 16): lane l holds keys
+  // 16j + 4*g16 + r (r < 4) of query row c16; the row's other 24 scores
+  // sit in the lanes 16, 32 and 48 apart.
+  auto qk16 = [&](int t, float4_v (&s)[2]) {
+    const int buf = t & 1;
+    s[0] = float4_v{0.0f, 0.0f, 0.0f, 0.0f};
+    s[1] = s[0];
+#pragma unroll
+    for (int kk = 0; kk < KS16; ++kk) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const half8_v a =
+            *reinterpret_cast<const half8_v *>(&s_k[buf][0][16 * j + c16][32 * kk + 8 * g16]);
+        s[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qop16[kk], s[j], 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int kk = 0; kk < KS16; ++kk) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    }
+  };
+  // Max / sum over the four lanes of a query row (lanes 16 apart).
+  auto row4_max = [](float v) {
+    v = fmaxf(v, __shfl_xor(v, 16, k_wave));
+    return fmaxf(v, __shfl_xor(v, 32, k_wave));
+  };
+  auto row4_sum = [](float v) {
+    v += __shfl_xor(v, 16, k_wave);
+    return v + __shfl_xor(v, 32, k_wave);
+  };
+  auto softmax16 = [&]<bool INTERIOR>(int t, float4_v (&s)[2]) {
+    if constexpr (!INTERIOR) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = t * KT + 16 * j + 4 * g16 + r;
+          bool ok = key <= my_pos && key < total;
+          if (!clean) {
+            const int lb = bt_shift >= 0 ? key >> bt_shift : key / bt;
+            ok = ok && lb < n_pt && s_ptab[lb] != 0xFFFFu;
+          }
+          s[j][r] = ok ? s[j][r] : -INFINITY;
+        }
+      }
+    }
+    float tmax = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
+                       fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
+    tmax = row4_max(tmax);
+    const bool need = tmax > m + rescale_raw;
+    float alpha = 1.0f;
+    if (need) {
+      alpha = fast_exp2((m - tmax) * P.c);  // 0 while the row had no valid key yet
+      l *= alpha;
+      m = tmax;
+    }
+    const float mc = m * P.c;
+    float psum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float pr = fast_exp2(fmaf(s[j][r], P.c, -mc));
+        s[j][r] = (INTERIOR || s[j][r] != -INFINITY) ? pr : 0.0f;
+      }
+      psum += (s[j][0] + s[j][1]) + (s[j][2] + s[j][3]);
+    }
+    l += row4_sum(psum);
+    if (__builtin_amdgcn_ballot_w64(need) != 0) {
+      // alpha of the O rows 4*g16 + r of this lane: from the lanes that own
+      // those query rows, through LDS (wave-private slice)
+      if (g16 == 0) s_row[wave][c16] = alpha;
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      __builtin_amdgcn_wave_barrier();
+      const float4_t ar = *reinterpret_cast<const float4_t *>(&s_row[wave][4 * g16]);
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int c = 0; c < OT16; ++c) {
+        o16[c][0] *= ar.x;
+        o16[c][1] *= ar.y;
+        o16[c][2] *= ar.z;
+        o16[c][3] *= ar.w;
+      }
+    }
+  };
+  // O (16 rows x D) += P (16 x 32 keys) . V (32 x D); the P operand of lane l
+  // is its own 8 probabilities, in the slot order the V^T staging used.
+  auto pv16 = [&](int t, const float4_v (&s)[2]) {
+    const int buf = t % VR;
+    half8_v pa;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      pa[r] = static_cast<half_t>(s[0][r]);
+      pa[4 + r] = static_cast<half_t>(s[1][r]);
+    }
+#pragma unroll
+    for (int c = 0; c < OT16; ++c) {
+      const half8_v b =
+          *reinterpret_cast<const half8_v *>(&s_vt[buf][0][16 * c + c16][8 * g16]);
+      o16[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, b, o16[c], 0, 0, 0);
+    }
+  };
+
   stage_t R;
   load_tile(0, R);
   store_tile(0, 0, R);
@@ -689,12 +831,19 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
   float16_v s[NS];
   // tiles [0, n_int) need no mask
   const int n_int = clean ? min(n_tiles, min((wg_first_pos + 1) / KT, total / KT)) : 0;
+  float4_v s16[2];
   auto step = [&]<bool INTERIOR>(int t) {
     const bool more = t + 1 < n_tiles;
     if (more) load_tile(t + 1, R);
-    qk(t, s);
-    softmax.template operator()<INTERIOR>(t, s);
-    pv(t, s);
+    if constexpr (M16) {
+      qk16(t, s16);
+      softmax16.template operator()<INTERIOR>(t, s16);
+      pv16(t, s16);
+    } else {
+      qk(t, s);
+      softmax.template operator()<INTERIOR>(t, s);
+      pv(t, s);
+    }
     if (more) store_tile((t + 1) & 1, (t + 1) % VR, R);
     __syncthreads();
   };
@@ -702,6 +851,23 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
   for (int t = n_int; t < n_tiles; ++t) step.template operator()<false>(t);
 
   // normalise by l of each row and write rows < n_q
+  if constexpr (M16) {
+    __builtin_amdgcn_wave_barrier();
+    if (g16 == 0) s_row[wave][c16] = l > 0.0f ? 1.0f / l : 0.0f;
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+    const float4_t inv = *reinterpret_cast<const float4_t *>(&s_row[wave][4 * g16]);
+    const float invs[4] = {inv.x, inv.y, inv.z, inv.w};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = row0 + 4 * g16 + r;
+      if (row >= n_q) continue;
+      float *op = P.out + ((static_cast<uint64_t>(seq) * n_q + row) * P.L.n_head + head) * D;
+#pragma unroll
+      for (int c = 0; c < OT16; ++c) op[16 * c + c16] = o16[c][r] * invs[r];
+    }
+    return;
+  }
   __builtin_amdgcn_wave_barrier();
   if (h == 0) s_row[wave][l32] = l > 0.0f ? 1.0f / l : 0.0f;
   __builtin_amdgcn_s_waitcnt(0xc07f);
@@ -717,7 +883,7 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
   }
 }
 
-template <int D, int KT, bool Q8>
+template <int D, int KT, bool Q8, bool M16 = false>
 bool launch_prefill_kt(const prefill_params &P, int32_t n_seq, hipStream_t st) {
   // W waves per workgroup: G_WG query heads of one KV group x RB blocks of
   // 32 query rows, all sharing each staged K/V tile.  head_dim 256 runs 4
@@ -727,13 +893,14 @@ bool launch_prefill_kt(const prefill_params &P, int32_t n_seq, hipStream_t st) {
   const int group = P.L.n_head / P.L.n_head_kv;
   const int g_wg = group < W ? group : W;
   const int rb = W / g_wg;
-  const int n_qt = (P.n_q + 32 * rb - 1) / (32 * rb);
+  constexpr int ROWS = M16 ? 16 : 32;
+  const int n_qt = (P.n_q + ROWS * rb - 1) / (ROWS * rb);
   const dim3 grid(n_qt * (P.L.n_head / g_wg) * n_seq);
   const dim3 block(W * k_wave);
   switch (g_wg) {
-    case 1: hipLaunchKernelGGL((prefill_kernel<D, 1, W, KT, Q8>), grid, block, 0, st, P); return true;
-    case 2: hipLaunchKernelGGL((prefill_kernel<D, 2, W / 2, KT, Q8>), grid, block, 0, st, P); return true;
-    case 4: hipLaunchKernelGGL((prefill_kernel<D, 4, W / 4, KT, Q8>), grid, block, 0, st, P); return true;
+    case 1: hipLaunchKernelGGL((prefill_kernel<D, 1, W, KT, Q8, M16>), grid, block, 0, st, P); return true;
+    case 2: hipLaunchKernelGGL((prefill_kernel<D, 2, W / 2, KT, Q8, M16>), grid, block, 0, st, P); return true;
+    case 4: hipLaunchKernelGGL((prefill_kernel<D, 4, W / 4, KT, Q8, M16>), grid, block, 0, st, P); return true;
     case 8:
       if constexpr (W == 8) {
         hipLaunchKernelGGL((prefill_kernel<D, 8, 1, KT, Q8>), grid, block, 0, st, P);
@@ -773,12 +940,13 @@ extern "C" emel_error_type emelk_attn_prefill_chunk(const emelk_kv_geometry *g, 
       !std::isfinite(scale)) {
     return EMELK_ERR_INVALID_REQUEST;
   }
-  if (L.head_dim == 512) {
-    // head_dim 512: row by row through the decode kernel, as the reference's
-    // per-row loop does.  One wave's 32 x 512 O tile and Q^T operand take
-    // 384 of its 512 registers; built that way the kernel spills about
-    // 1500 registers per lane, and with wave pairs that split O's columns
-    // (each still holding the 128-register Q^T operand) about 350.
+  if (L.head_dim == 512 && L.kv_type == EMELK_KV_Q8_0) {
+    // q8_0 at head_dim 512: row by row through the decode kernel, as the
+    // reference's per-row loop does (the hi/lo planes do not fit the LDS).
+    // f16 pools at 512 run 16 query rows per wave (M16): a wave's 32 x 512
+    // O tile and Q^T operand take 384 of its 512 registers, and built that
+    // way the kernel spills about 1500 registers per lane (about 350 with
+    // wave pairs that split O's columns).
     return emelk::decode_rows(L, k_pool, v_pool, layer, q, out, n_seq, n_q, q_start,
                               block_tables, table_stride, scale, static_cast<hipStream_t>(stream));
   }
@@ -802,7 +970,8 @@ extern "C" emel_error_type emelk_attn_prefill_chunk(const emelk_kv_geometry *g, 
   const bool q8 = L.kv_type == EMELK_KV_Q8_0;
   // head_dim 256: 32-key tiles (64 spill, and q8_0's hi/lo planes of 64-key
   // tiles would not fit the LDS)
-  const bool ok = L.head_dim == 256
+  const bool ok = L.head_dim == 512 ? emelk::launch_prefill_kt<512, 32, false, true>(P, n_seq, st)
+                  : L.head_dim == 256
                       ? (q8 ? emelk::launch_prefill_kt<256, 32, true>(P, n_seq, st)
                             : emelk::launch_prefill_kt<256, 32, false>(P, n_seq, st))
                   : L.head_dim == 128 ? emelk::launch_prefill<128>(P, n_seq, st)

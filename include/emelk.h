@@ -200,7 +200,7 @@ typedef struct emelk_kv_geometry {
   int32_t n_layer;
   int32_t n_head;      /* query heads */
   int32_t n_head_kv;   /* key/value heads (GQA: n_head % n_head_kv == 0) */
-  int32_t head_dim;    /* 64, 128, 256 or 512 (512: prefill runs row by row) */
+  int32_t head_dim;    /* 64, 128, 256 or 512 (q8_0 at 512: prefill runs row by row) */
   int32_t block_tokens;/* tokens per page */
   int32_t max_blocks;  /* pages in the pool */
   int32_t kv_type;     /* EMELK_KV_F16 or EMELK_KV_Q8_0 */
@@ -280,10 +280,11 @@ emel_error_type emelk_attn_decode_append(const emelk_kv_geometry *g, void *k_poo
  * Replaces the per-row store + attend loop of run_prefill
  * (text/generator/detail.hpp:4297-4372).  head_dim 64 and 128 run on MFMA,
  * f16 and q8_0 pools alike (q8_0 values enter the MFMAs exactly, as two
- * fp16 parts; values of magnitude 65520 or more do not fit), and so does
- * head_dim 256.  head_dim 512 runs row by row through the decode kernel
- * (n_seq * n_q <= 65535, and a row's context, table_stride * block_tokens
- * tokens at most, must fit 1022 pages). */
+ * fp16 parts; values of magnitude 65520 or more do not fit), and so do
+ * head_dim 256 and, on f16 pools, 512.  q8_0 at head_dim 512 runs row by
+ * row through the decode kernel (n_seq * n_q <= 65535, and a row's
+ * context, table_stride * block_tokens tokens at most, must fit 1022
+ * pages). */
 emel_error_type emelk_attn_prefill_chunk(const emelk_kv_geometry *g, const void *k_pool,
                                          const void *v_pool, int32_t layer, const float *q,
                                          float *out, int32_t n_seq, int32_t n_q,

@@ -689,6 +689,7 @@ Q8_PREFILL_CASES = [
     (8, 2, 128, 16, [100, 37], 40, (1, 2)),
     (8, 1, 256, 16, [40], 9, None),               # head_dim 256: 4 waves, 32-key tiles
     (8, 2, 256, 32, [70, 3], 36, (0, 1)),         # head_dim 256, NaN pool, invalid page
+    (8, 1, 512, 16, [30], 11, None),              # head_dim 512: row by row
 ]
 
 
@@ -809,10 +810,17 @@ def test_prefill_chunk_head_dim_256(device, n_head, n_kv, bt, q_starts, n_q):
     _prefill_case(device, n_head, n_kv, 256, bt, q_starts, n_q, seed=81)
 
 
-def test_prefill_chunk_head_dim_512_row_route(device):
-    # head_dim 512 takes the row-by-row route through the decode kernel
-    banner("prefill chunk at head_dim 512 (row by row)")
-    _prefill_case(device, 8, 2, 512, 16, [0, 70], 13, seed=82)
+@pytest.mark.parametrize("n_head,n_kv,bt,q_starts,n_q", [
+    (8, 2, 16, [0, 70], 13),       # G=4, general staging
+    (8, 1, 32, [40], 50),          # G=8 (Gemma-4 global layers): two workgroups per row block
+    (4, 4, 32, [9, 100], 35),      # G=1: 4 row blocks per workgroup
+    (8, 4, 32, [64], 20),          # G=2
+])
+def test_prefill_chunk_head_dim_512(device, n_head, n_kv, bt, q_starts, n_q):
+    """head_dim 512 on the MFMA kernel with 16 query rows per wave
+    (v_mfma_f32_16x16x32_f16), 4 waves per workgroup."""
+    banner(f"prefill chunk at head_dim 512 H={n_head}/{n_kv} bt={bt} starts={q_starts} n_q={n_q}")
+    _prefill_case(device, n_head, n_kv, 512, bt, q_starts, n_q, seed=82)
 
 
 def test_decode_straight_from_the_device_view(device):
