@@ -890,6 +890,7 @@ bool launch_prefill_kt(const prefill_params &P, int32_t n_seq, hipStream_t st) {
   // waves, one per SIMD, so each has the full register file for its 32 x
   // 256 O tile and Q^T operand (8 waves at head_dim <= 128).
   constexpr int W = D > 128 ? 4 : 8;
+  static_assert(!M16 || W == 4, "M16 runs 4 waves per workgroup");
   const int group = P.L.n_head / P.L.n_head_kv;
   const int g_wg = group < W ? group : W;
   const int rb = W / g_wg;
@@ -903,7 +904,7 @@ bool launch_prefill_kt(const prefill_params &P, int32_t n_seq, hipStream_t st) {
     case 4: hipLaunchKernelGGL((prefill_kernel<D, 4, W / 4, KT, Q8, M16>), grid, block, 0, st, P); return true;
     case 8:
       if constexpr (W == 8) {
-        hipLaunchKernelGGL((prefill_kernel<D, 8, 1, KT, Q8>), grid, block, 0, st, P);
+        hipLaunchKernelGGL((prefill_kernel<D, 8, 1, KT, Q8, M16>), grid, block, 0, st, P);
         return true;
       }
       return false;
