@@ -47,6 +47,7 @@ PMC_TRAFFIC_BYTES = {
     "llama3-8b-q8_0-prefill512-evict25": 214867558,
     "gemma4-d256-prefill512-evict25": 105300848,
     "gemma4-d256-q8_0-prefill512-evict25": 87748528,
+    "gemma4-d512-prefill512-evict25": 285765904,
 }
 
 CONFIGS = {
