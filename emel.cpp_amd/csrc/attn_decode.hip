@@ -29,6 +29,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <atomic>
 #include <cstdlib>
 
 #include "device_common.hpp"
@@ -771,27 +772,23 @@ struct decode_plan {
   uint64_t workspace_bytes = 0;
 };
 
-int32_t env_int(const char *name, int32_t fallback) {
-  const char *v = std::getenv(name);
-  if (v == nullptr || *v == 0) return fallback;
-  const long x = std::strtol(v, nullptr, 10);
-  return x > 0 ? static_cast<int32_t>(x) : fallback;
-}
-
-// Compute units of the current device (cached per device id).
+// Compute units of the current device, cached per device id.  Racing first
+// calls store the same value, so relaxed atomics are enough.
 int32_t device_cu_count() {
-  static int32_t cached[64] = {0};
+  static std::atomic<int32_t> cached[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        cus <= 0) {
-      cus = 256;
+  int32_t cus = cached[dev].load(std::memory_order_relaxed);
+  if (cus == 0) {
+    int c = 0;
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        c <= 0) {
+      c = 256;
     }
-    cached[dev] = cus;
+    cus = c;
+    cached[dev].store(cus, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return cus;
 }
 
 // A balanced plan (every wave derives splits of equal size over all tokens
@@ -811,12 +808,10 @@ decode_plan plan_decode(const pool_layout &L, int32_t n_seq, int32_t max_kv_len)
   const int32_t tile = 2 * (k_wave / lpt);
   const int32_t wpb = waves_per_block(L.n_head_kv);
   const int32_t units = n_seq * (L.n_head_kv / wpb);
-  const int32_t target = env_int("EMELK_DECODE_TARGET_WG", device_cu_count());
+  const int32_t target = device_cu_count();
   const int32_t tiles = (max_kv_len + tile - 1) / tile;
   int32_t splits = (target + units - 1) / units;
   splits = splits < 1 ? 1 : (splits > tiles ? tiles : splits);
-  const int32_t forced = env_int("EMELK_DECODE_SPLITS", 0);
-  if (forced > 0) splits = forced < tiles ? forced : tiles;
   int32_t tps = ((max_kv_len + splits - 1) / splits + tile - 1) / tile * tile;
   const int32_t max_tps = ((k_max_split_pages - 2) * L.block_tokens) / tile * tile;
   if (tps > max_tps) tps = max_tps;
@@ -948,15 +943,52 @@ emel_error_type decode_rows(const pool_layout &L, const void *k_pool, const void
 
 }  // namespace emelk
 
+// The split count grows as the batch shrinks (about one workgroup per CU is
+// the target), so n_seq * splits is not monotone in n_seq.  A workspace sized
+// for (n_seq, max_kv_len) must serve every call with fewer sequences or
+// shorter contexts, which is what an executor sized for its largest step
+// relies on; the size returned is the maximum of the exact need over all
+// n' <= n_seq, len' <= max_kv_len.  For a fixed n', splits(n', len') <=
+// max(min(ceil(target / units'), tiles(len')), ceil(len' / max_tps)), which
+// is nondecreasing in len', so the bound at len' = max_kv_len covers them.
 extern "C" emel_error_type emelk_attn_decode_workspace_size(const emelk_kv_geometry *g,
                                                             int32_t n_seq, int32_t max_kv_len,
                                                             uint64_t *bytes_out) {
   emelk::pool_layout L;
   if (emelk::make_pool_layout(g, L) != EMELK_ERR_NONE || bytes_out == nullptr || n_seq <= 0 ||
+      n_seq > 65535 || max_kv_len <= 0) {
+    return EMELK_ERR_INVALID_REQUEST;
+  }
+  const int32_t tile = 2 * (emelk::k_wave / (L.head_dim / 16));
+  const int32_t wpb = emelk::waves_per_block(L.n_head_kv);
+  const int32_t target = emelk::device_cu_count();
+  const int64_t tiles = (static_cast<int64_t>(max_kv_len) + tile - 1) / tile;
+  const int64_t max_tps = ((emelk::k_max_split_pages - 2) * L.block_tokens) / tile * tile;
+  const int64_t clamp_splits = (max_kv_len + max_tps - 1) / max_tps;
+  uint64_t worst = 0;
+  for (int64_t n = 1; n <= n_seq; ++n) {
+    const int64_t units = n * (L.n_head_kv / wpb);
+    int64_t splits = (target + units - 1) / units;
+    if (splits > tiles) splits = tiles;
+    if (splits < clamp_splits) splits = clamp_splits;
+    if (static_cast<uint64_t>(n * splits) > worst) worst = static_cast<uint64_t>(n * splits);
+  }
+  *bytes_out = worst * L.n_head * static_cast<uint64_t>(L.head_dim + 2) * sizeof(float);
+  return EMELK_ERR_NONE;
+}
+
+extern "C" emel_error_type emelk_attn_decode_plan(const emelk_kv_geometry *g, int32_t n_seq,
+                                                  int32_t max_kv_len, int32_t *tokens_per_split,
+                                                  int32_t *n_splits, uint64_t *bytes_out) {
+  emelk::pool_layout L;
+  if (emelk::make_pool_layout(g, L) != EMELK_ERR_NONE || n_seq <= 0 || n_seq > 65535 ||
       max_kv_len <= 0) {
     return EMELK_ERR_INVALID_REQUEST;
   }
-  *bytes_out = emelk::plan_decode(L, n_seq, max_kv_len).workspace_bytes;
+  const emelk::decode_plan p = emelk::plan_decode(L, n_seq, max_kv_len);
+  if (tokens_per_split != nullptr) *tokens_per_split = p.tokens_per_split;
+  if (n_splits != nullptr) *n_splits = p.max_splits;
+  if (bytes_out != nullptr) *bytes_out = p.workspace_bytes;
   return EMELK_ERR_NONE;
 }
 

@@ -172,9 +172,12 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
   const int g16 = lane / 16;  // M16: lane group
   const int n_q = P.n_q;
   const int q0 = P.q_start[seq];
-  const int total = q0 + n_q;
+  // a negative q_start names no valid position: the sequence attends to
+  // nothing (no tiles, no page lookups) and its rows are written as zeros
+  const bool seq_ok = q0 >= 0;
+  const int total = seq_ok ? q0 + n_q : 0;
   const int wg_row_end = min(n_q, (qt + 1) * RB * ROWS);
-  const int key_end = q0 + wg_row_end;  // exclusive
+  const int key_end = seq_ok ? q0 + wg_row_end : 0;  // exclusive
   const int n_tiles = (key_end + KT - 1) / KT;
   const int my_row = row0 + (M16 ? c16 : l32);
   const bool row_ok = my_row < n_q;

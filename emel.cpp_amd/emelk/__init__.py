@@ -212,6 +212,9 @@ _SIGNATURES = [
      [ctypes.POINTER(Geometry), _P, _P, _P, ctypes.c_int32, _P]),
     ("emelk_attn_decode_workspace_size", ctypes.c_uint32,
      [ctypes.POINTER(Geometry), ctypes.c_int32, ctypes.c_int32, ctypes.POINTER(ctypes.c_uint64)]),
+    ("emelk_attn_decode_plan", ctypes.c_uint32,
+     [ctypes.POINTER(Geometry), ctypes.c_int32, ctypes.c_int32, c_i32p, c_i32p,
+      ctypes.POINTER(ctypes.c_uint64)]),
     ("emelk_attn_decode", ctypes.c_uint32,
      [ctypes.POINTER(Geometry), _P, _P, ctypes.c_int32, _P, _P, ctypes.c_int32, _P,
       ctypes.c_int32, _P, ctypes.c_int32, ctypes.c_float, _P, ctypes.c_uint64, _P]),
@@ -423,6 +426,69 @@ def _ptr(t):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
+# Tensor checks run before every device call: a tensor of the wrong dtype,
+# device, layout or size would otherwise become an out-of-bounds device read
+# or write instead of a Python error.  Objects that only carry data_ptr()
+# (DevPtr, library-owned pools) are raw addresses the caller vouches for.
+_I16 = ("int16", "uint16")
+
+
+def _is_tensor(t):
+    return hasattr(t, "is_cuda") and hasattr(t, "dtype")
+
+
+def _need(t, name, dtypes=None, shape=None, min_bytes=None, optional=False):
+    if t is None:
+        if optional:
+            return
+        raise ValueError(f"{name}: a device tensor is required")
+    if not _is_tensor(t):
+        if hasattr(t, "data_ptr"):
+            return
+        raise TypeError(f"{name}: expected a device tensor, got {type(t).__name__}")
+    if not t.is_cuda:
+        raise ValueError(f"{name}: tensor must be on the GPU (got device {t.device})")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: tensor must be contiguous")
+    if dtypes is not None:
+        dt = str(t.dtype).replace("torch.", "")
+        if dt not in dtypes:
+            raise TypeError(f"{name}: dtype {dt}, expected {' or '.join(dtypes)}")
+    if shape is not None:
+        got = tuple(int(x) for x in t.shape)
+        want = tuple(shape)
+        if len(got) != len(want) or any(w is not None and w != x for w, x in zip(want, got)):
+            raise ValueError(f"{name}: shape {got}, expected {want} (None = any)")
+    if min_bytes is not None and t.numel() * t.element_size() < min_bytes:
+        raise ValueError(f"{name}: {t.numel() * t.element_size()} bytes, need {min_bytes}")
+
+
+def _pools(g, k_pool, v_pool):
+    pb = pool_bytes(g)
+    _need(k_pool, "k_pool", min_bytes=pb)
+    _need(v_pool, "v_pool", min_bytes=pb)
+
+
+def _numel(t):
+    n = 1
+    for x in t.shape:
+        n *= int(x)
+    return n
+
+
+def _rows(t, name, n_seq, n_tokens, width):
+    """fp32 rows [n_seq][n_tokens][width], given as 3-D or flattened."""
+    _need(t, name, ("float32",))
+    if _is_tensor(t) and _numel(t) != n_seq * n_tokens * width:
+        raise ValueError(f"{name}: {_numel(t)} floats, expected {n_seq}*{n_tokens}*{width}")
+
+
+def _tables(t, n_seq):
+    _need(t, "block_tables", _I16)
+    if _is_tensor(t) and (t.dim() != 2 or int(t.shape[0]) < n_seq):
+        raise ValueError(f"block_tables: shape {tuple(t.shape)}, expected [>= {n_seq}, stride]")
+
+
 def _stream(stream):
     if stream is not None:
         return ctypes.c_void_p(stream)
@@ -438,6 +504,12 @@ def _check(e, what):
 def append(g, k_pool, v_pool, layer, k_rows, v_rows, positions, block_tables, stream=None):
     """k_rows/v_rows: float32 [n_seq, n_tokens, n_head_kv*head_dim] on the device."""
     n_seq, n_tokens = int(k_rows.shape[0]), int(k_rows.shape[1])
+    kvd = g.n_head_kv * g.head_dim
+    _pools(g, k_pool, v_pool)
+    _rows(k_rows, "k_rows", n_seq, n_tokens, kvd)
+    _rows(v_rows, "v_rows", n_seq, n_tokens, kvd)
+    _need(positions, "positions", ("int32",), (n_seq,))
+    _tables(block_tables, n_seq)
     _check(lib.emelk_kv_append(ctypes.byref(g), _ptr(k_pool), _ptr(v_pool), layer, _ptr(k_rows),
                                _ptr(v_rows), n_seq, n_tokens, _ptr(positions), _ptr(block_tables),
                                int(block_tables.shape[1]), _stream(stream)), "emelk_kv_append")
@@ -445,6 +517,13 @@ def append(g, k_pool, v_pool, layer, k_rows, v_rows, positions, block_tables, st
 
 def gather(g, k_pool, v_pool, layer, lengths, block_tables, k_out, v_out, out_tokens,
            stream=None):
+    n_seq = int(lengths.shape[0])
+    _pools(g, k_pool, v_pool)
+    _need(lengths, "lengths", ("int32",), (n_seq,))
+    _tables(block_tables, n_seq)
+    row = g.n_head_kv * g.head_dim * 2 if g.kv_type == KV_F16 else g.n_head_kv * g.head_dim // 32 * 34
+    _need(k_out, "k_out", min_bytes=n_seq * out_tokens * row)
+    _need(v_out, "v_out", min_bytes=n_seq * out_tokens * row)
     _check(lib.emelk_kv_gather(ctypes.byref(g), _ptr(k_pool), _ptr(v_pool), layer,
                                int(lengths.shape[0]), _ptr(lengths), _ptr(block_tables),
                                int(block_tables.shape[1]), _ptr(k_out), _ptr(v_out), out_tokens,
@@ -453,6 +532,8 @@ def gather(g, k_pool, v_pool, layer, lengths, block_tables, k_out, v_out, out_to
 
 def copy_blocks(g, k_pool, v_pool, moves, stream=None):
     """moves: int32 [n, 2] device tensor of (src, dst) page ids."""
+    _pools(g, k_pool, v_pool)
+    _need(moves, "moves", ("int32",), (None, 2))
     _check(lib.emelk_kv_copy_blocks(ctypes.byref(g), _ptr(k_pool), _ptr(v_pool), _ptr(moves),
                                     int(moves.shape[0]), _stream(stream)),
            "emelk_kv_copy_blocks")
@@ -465,8 +546,29 @@ def decode_workspace_bytes(g, n_seq, max_kv_len) -> int:
     return int(out.value)
 
 
+def decode_plan(g, n_seq, max_kv_len):
+    """(tokens_per_split, n_splits, workspace_bytes) of one decode call."""
+    tps, ns, b = ctypes.c_int32(0), ctypes.c_int32(0), ctypes.c_uint64(0)
+    _check(lib.emelk_attn_decode_plan(ctypes.byref(g), n_seq, max_kv_len, ctypes.byref(tps),
+                                      ctypes.byref(ns), ctypes.byref(b)), "decode_plan")
+    return tps.value, ns.value, int(b.value)
+
+
+def _decode_args(g, k_pool, v_pool, q, out, kv_lens, block_tables, workspace):
+    _pools(g, k_pool, v_pool)
+    if not _is_tensor(q):
+        raise TypeError("q: expected a device tensor (its first dimension is n_seq)")
+    n_seq = int(q.shape[0])
+    _rows(q, "q", n_seq, g.n_head, g.head_dim)
+    _rows(out, "out", n_seq, g.n_head, g.head_dim)
+    _need(kv_lens, "kv_lens", ("int32",), (n_seq,))
+    _tables(block_tables, n_seq)
+    _need(workspace, "workspace")
+
+
 def decode(g, k_pool, v_pool, layer, q, out, kv_lens, max_kv_len, block_tables, scale,
            workspace, stream=None):
+    _decode_args(g, k_pool, v_pool, q, out, kv_lens, block_tables, workspace)
     _check(lib.emelk_attn_decode(ctypes.byref(g), _ptr(k_pool), _ptr(v_pool), layer, _ptr(q),
                                  _ptr(out), int(q.shape[0]), _ptr(kv_lens), max_kv_len,
                                  _ptr(block_tables), int(block_tables.shape[1]), scale,
@@ -478,6 +580,10 @@ def decode_append(g, k_pool, v_pool, layer, k_rows, v_rows, q, out, kv_lens, max
                   block_tables, scale, workspace, stream=None):
     """Store the token at position kv_lens - 1 (k_rows/v_rows float32
     [n_seq, n_head_kv*head_dim]) and attend over kv_lens tokens, one launch."""
+    _decode_args(g, k_pool, v_pool, q, out, kv_lens, block_tables, workspace)
+    n_seq = int(q.shape[0])
+    _rows(k_rows, "k_rows", n_seq, 1, g.n_head_kv * g.head_dim)
+    _rows(v_rows, "v_rows", n_seq, 1, g.n_head_kv * g.head_dim)
     _check(lib.emelk_attn_decode_append(ctypes.byref(g), _ptr(k_pool), _ptr(v_pool), layer,
                                         _ptr(k_rows), _ptr(v_rows), _ptr(q), _ptr(out),
                                         int(q.shape[0]), _ptr(kv_lens), max_kv_len,
@@ -489,6 +595,14 @@ def decode_append(g, k_pool, v_pool, layer, k_rows, v_rows, q, out, kv_lens, max
 
 def prefill_chunk(g, k_pool, v_pool, layer, q, out, q_start, block_tables, scale, stream=None):
     """q/out: float32 [n_seq, n_q, n_head, head_dim]."""
+    _pools(g, k_pool, v_pool)
+    if not _is_tensor(q) or q.dim() < 2:
+        raise TypeError("q: expected a device tensor [n_seq, n_q, ...]")
+    n_seq, n_q = int(q.shape[0]), int(q.shape[1])
+    _rows(q, "q", n_seq, n_q, g.n_head * g.head_dim)
+    _rows(out, "out", n_seq, n_q, g.n_head * g.head_dim)
+    _need(q_start, "q_start", ("int32",), (n_seq,))
+    _tables(block_tables, n_seq)
     _check(lib.emelk_attn_prefill_chunk(ctypes.byref(g), _ptr(k_pool), _ptr(v_pool), layer,
                                         _ptr(q), _ptr(out), int(q.shape[0]), int(q.shape[1]),
                                         _ptr(q_start), _ptr(block_tables),
@@ -524,6 +638,15 @@ def qkv_rope_append(g, k_pool, v_pool, layer, q_in, q_out, k_rows, v_rows, posit
     """q_in/q_out: float32 [n_seq, n_tokens, n_head*head_dim]; k_rows/v_rows:
     float32 [n_seq, n_tokens, n_head_kv*head_dim]; all on the device."""
     n_seq, n_tokens = int(k_rows.shape[0]), int(k_rows.shape[1])
+    _pools(g, k_pool, v_pool)
+    _rows(q_in, "q_in", n_seq, n_tokens, g.n_head * g.head_dim)
+    _rows(q_out, "q_out", n_seq, n_tokens, g.n_head * g.head_dim)
+    _rows(k_rows, "k_rows", n_seq, n_tokens, g.n_head_kv * g.head_dim)
+    _rows(v_rows, "v_rows", n_seq, n_tokens, g.n_head_kv * g.head_dim)
+    _need(positions, "positions", ("int32",), (n_seq,))
+    _tables(block_tables, n_seq)
+    _need(q_norm, "q_norm", ("float32",), (g.head_dim,), optional=True)
+    _need(k_norm, "k_norm", ("float32",), (g.head_dim,), optional=True)
     _check(lib.emelk_kv_qkv_rope_append(
         ctypes.byref(g), _ptr(k_pool), _ptr(v_pool), layer, _ptr(q_in), _ptr(q_out),
         _ptr(k_rows), _ptr(v_rows), n_seq, n_tokens, _ptr(positions), _ptr(block_tables),

@@ -249,9 +249,18 @@ emel_error_type emelk_kv_copy_blocks(const emelk_kv_geometry *g, void *k_pool, v
  * to fp16 on load, as round_q_for_nonflash does); out: fp32, same shape.
  * kv_lens: device int32 [n_seq], tokens to attend (position + 1), each in
  * [1, max_kv_len].  scale multiplies q.k.  workspace: device scratch of
- * emelk_attn_decode_workspace_size bytes. */
+ * emelk_attn_decode_workspace_size bytes.
+ * emelk_attn_decode_workspace_size(n_seq, max_kv_len) is enough for every
+ * call with at most n_seq sequences and max_kv_len at most max_kv_len (the
+ * split count rises as the batch shrinks, so the exact need of one call is
+ * not monotone in n_seq); emelk_attn_decode_plan reports the exact split
+ * plan and workspace need of one call with these arguments.  The reference
+ * has no counterpart: its CPU route needs no partials. */
 emel_error_type emelk_attn_decode_workspace_size(const emelk_kv_geometry *g, int32_t n_seq,
                                                  int32_t max_kv_len, uint64_t *bytes_out);
+emel_error_type emelk_attn_decode_plan(const emelk_kv_geometry *g, int32_t n_seq,
+                                       int32_t max_kv_len, int32_t *tokens_per_split,
+                                       int32_t *n_splits, uint64_t *bytes_out);
 emel_error_type emelk_attn_decode(const emelk_kv_geometry *g, const void *k_pool,
                                   const void *v_pool, int32_t layer, const float *q, float *out,
                                   int32_t n_seq, const int32_t *kv_lens, int32_t max_kv_len,

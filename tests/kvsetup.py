@@ -183,3 +183,8 @@ def assert_close(got, want, atol=2e-3, rtol=1e-2, what=""):
     assert not bad.any(), (f"{what}: {bad.sum()} of {bad.size} outside tolerance; "
                            f"max abs err {err.max():.3e}")
     return float(err.max())
+
+
+def banner(msg):
+    """Names the case on stdout before any GPU work, flushed."""
+    print(f"\n[gpu-case] {msg}", flush=True)

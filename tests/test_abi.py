@@ -102,3 +102,98 @@ def test_plain_c_client_builds_and_runs(tmp_path):
                     "-L", libdir, "-lemelk", f"-Wl,-rpath,{libdir}", "-o", exe], check=True)
     res = subprocess.run([exe], capture_output=True, text=True, timeout=60)
     assert res.returncode == 0 and res.stdout.strip() == "ok", res.stdout + res.stderr
+
+
+def test_workspace_size_covers_every_smaller_call():
+    """A workspace sized for (n_seq, max_kv_len) must serve every call with
+    fewer sequences or shorter contexts: an executor sizes it once for its
+    largest step.  The split count rises as the batch shrinks, so the exact
+    need (emelk_attn_decode_plan) is not monotone in n_seq."""
+    lens = [1, 31, 32, 33, 500, 1023, 1024, 1025, 4096, 8191, 8192]
+    for g in (emelk.geometry(32, 32, 8, 128, 32, 16448),
+              emelk.geometry(16, 32, 8, 64, 16, 32768),
+              emelk.geometry(28, 16, 8, 128, 32, 64, emelk.KV_Q8_0),
+              emelk.geometry(4, 8, 1, 512, 16, 2048)):
+        exact = {(n, L): emelk.decode_plan(g, n, L)[2] for n in range(1, 65) for L in lens}
+        non_monotone = any(exact[(n, 8192)] > exact[(64, 8192)] for n in range(1, 64))
+        for n_max in (1, 3, 16, 64):
+            for L_max in (33, 1024, 8192):
+                ws = emelk.decode_workspace_bytes(g, n_max, L_max)
+                need = max(v for (n, L), v in exact.items() if n <= n_max and L <= L_max)
+                assert ws >= need, (g.head_dim, n_max, L_max, ws, need)
+        if g.head_dim == 128 and g.n_head_kv == 8 and g.kv_type == emelk.KV_F16:
+            assert non_monotone  # the case the bound exists for
+
+
+def test_decode_plan_splits_cover_the_context():
+    g = emelk.geometry(32, 32, 8, 128, 32, 16448)
+    for n, L in [(1, 512), (3, 8192), (16, 4096), (64, 8192), (64, 1)]:
+        tps, ns, b = emelk.decode_plan(g, n, L)
+        assert tps > 0 and ns >= 1 and (ns - 1) * tps < L <= ns * tps
+        assert b == n * 32 * ns * (128 + 2) * 4
+
+
+class _FakeDev:
+    """Stands in for a device tensor so the checks can be driven on the CPU;
+    every case below must raise before any device call."""
+
+    def __init__(self, t, cuda=True):
+        self.t, self.is_cuda, self.dtype, self.shape = t, cuda, t.dtype, t.shape
+        self.device = "cuda:0" if cuda else "cpu"
+
+    def is_contiguous(self):
+        return self.t.is_contiguous()
+
+    def dim(self):
+        return self.t.dim()
+
+    def numel(self):
+        return self.t.numel()
+
+    def element_size(self):
+        return self.t.element_size()
+
+    def data_ptr(self):
+        raise AssertionError("validation let a bad call through to the library")
+
+
+def test_python_helpers_reject_bad_tensors_before_any_launch():
+    import pytest
+    import torch
+    g = emelk.geometry(2, 8, 2, 64, 16, 64)
+    pb = emelk.pool_bytes(g)
+    F = _FakeDev
+    kp, vp = F(torch.zeros(pb, dtype=torch.uint8)), F(torch.zeros(pb, dtype=torch.uint8))
+    q = F(torch.zeros(3, 8, 64))
+    out = F(torch.zeros(3, 8, 64))
+    lens = F(torch.zeros(3, dtype=torch.int32))
+    tables = F(torch.zeros(3, 4, dtype=torch.int16))
+    ws = F(torch.zeros(64))
+    cases = [
+        dict(k_pool=F(torch.zeros(pb - 1, dtype=torch.uint8))),     # pool too small
+        dict(q=F(torch.zeros(3, 8, 64), cuda=False)),               # host tensor
+        dict(q=F(torch.zeros(3, 8, 64, dtype=torch.float64))),      # dtype
+        dict(q=F(torch.zeros(64, 8, 3).transpose(0, 2))),           # not contiguous
+        dict(out=F(torch.zeros(3, 8, 32))),                         # shape
+        dict(kv_lens=F(torch.zeros(3, dtype=torch.int64))),         # index dtype
+        dict(kv_lens=F(torch.zeros(2, dtype=torch.int32))),         # one length short
+        dict(block_tables=F(torch.zeros(2, 4, dtype=torch.int16))),  # one row short
+        dict(block_tables=F(torch.zeros(3, 4, dtype=torch.int32))),  # table dtype
+        dict(workspace=None),
+    ]
+    base = dict(k_pool=kp, v_pool=vp, q=q, out=out, kv_lens=lens, block_tables=tables,
+                workspace=ws)
+    for case in cases:
+        a = dict(base, **case)
+        with pytest.raises((ValueError, TypeError)):
+            emelk.decode(g, a["k_pool"], a["v_pool"], 0, a["q"], a["out"], a["kv_lens"], 10,
+                         a["block_tables"], 0.125, a["workspace"])
+    rows = F(torch.zeros(3, 5, 2 * 64))
+    pos = F(torch.zeros(3, dtype=torch.int32))
+    with pytest.raises(ValueError):
+        emelk.append(g, kp, vp, 0, rows, F(torch.zeros(3, 5, 64)), pos, tables)
+    with pytest.raises(ValueError):
+        emelk.prefill_chunk(g, kp, vp, 0, F(torch.zeros(3, 5, 8, 64)), F(torch.zeros(3, 5, 8, 64)),
+                            F(torch.zeros(2, dtype=torch.int32)), tables, 0.125)
+    with pytest.raises(ValueError):
+        emelk.copy_blocks(g, kp, vp, F(torch.zeros(4, 3, dtype=torch.int32)))

@@ -311,3 +311,45 @@ def test_batch_decoder_decode_layers_replay_as_a_graph(device):
             graph.replay()
             check(r, pos, f"replay {step + 2}")
         dec.close()
+
+
+def test_batch_decoder_sized_for_64_runs_small_steps_on_a_fixed_plan(device):
+    """A decoder sized for 64 sequences must run steps of 3, 5, 6 and 7: with
+    the graph-stable plan (planned for max_kv_len) a small batch takes more
+    splits per sequence, and n_seq * splits exceeds 64 * splits(64) for
+    these batch sizes.  The workspace must cover every smaller call."""
+    import torch
+    banner("batch decoder: max_batch 64, steps of 3/5/6/7 sequences on a fixed plan")
+    rng = np.random.default_rng(17)
+    max_kv = 2048
+    g = emelk.geometry(L, H, HKV, D, BT, 256, emelk.KV_F16)
+    actor = emelk.KvActor()
+    assert actor.reserve(64, 256, BT)[0]
+    for s in range(7):
+        assert actor.allocate_sequence(s)[0]
+    cache = emelk.KvCache(g)
+    rope = emelk.RopeTable(D, D, max_kv, BASE, emelk.NEOX_PAIRING)
+    dec = emelk.BatchDecoder(g, actor, cache, rope, max_batch=64, max_kv_len=max_kv)
+    dec.set_fixed_plan(True)
+    model = Model()
+    for s in range(7):
+        model.ensure(s)
+    for ids, n_tok in (([0, 1, 2, 3, 4, 5, 6], 24), ([0, 1, 2], 1), ([0, 1, 2, 3, 4], 1),
+                       ([5, 4, 3, 2, 1, 0], 1), ([0, 1, 2, 3, 4, 5, 6], 1)):
+        pos = dec.begin_step(ids, n_tok)
+        n = len(ids)
+        for layer in range(L):
+            q = rng.standard_normal((n, n_tok, H * D)).astype(np.float32)
+            k = rng.standard_normal((n, n_tok, HKV * D)).astype(np.float32)
+            v = rng.standard_normal((n, n_tok, HKV * D)).astype(np.float32)
+            qd = torch.from_numpy(q).to(device)
+            out = torch.full((n, n_tok, H * D), float("nan"), device=device)
+            dec.layer(layer, qd, qd, torch.from_numpy(k).to(device),
+                      torch.from_numpy(v).to(device), out, SCALE)
+            torch.cuda.synchronize()
+            got = out.cpu().numpy()
+            for i, s in enumerate(ids):
+                for t in range(n_tok):
+                    want = model.token(s, layer, q[i, t], k[i, t], v[i, t], pos[i] + t, None, None)
+                    assert_close(got[i, t], want, what=f"n={n} layer {layer} seq {s} tok {t}")
+    dec.close()

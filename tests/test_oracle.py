@@ -249,3 +249,31 @@ def test_flash_f16acc_vs_nonflash_routes_agree_loosely():
     v = oracle.fp16_to_fp32(g["qwen3_v"]).transpose(1, 0, 2).reshape(T, HK * D)
     ideal = oracle.attention_f64(q, k, v, H, HK, D, T, float(g["qwen3_scale"]))
     assert np.max(np.abs(flash - ideal)) < 2e-2
+
+
+def test_decode_batch_threads_equal_per_sequence_route_bit_for_bit():
+    """orc_decode_batch_f16 (the bench's full-size checker and CPU baseline)
+    is the per-sequence route on worker threads: every thread count gives the
+    per-sequence outputs bit for bit, on ragged lengths over one shared
+    paged cache."""
+    rng = np.random.default_rng(11)
+    n_head, n_kv, D, bt, n_blocks, stride = 8, 2, 64, 16, 96, 8
+    kv_dim = n_kv * D
+    kc = oracle.fp32_to_fp16(rng.standard_normal((n_blocks * bt, kv_dim)).astype(np.float32))
+    vc = oracle.fp32_to_fp16(rng.standard_normal((n_blocks * bt, kv_dim)).astype(np.float32))
+    n_seq = 7
+    tables = np.stack([rng.permutation(n_blocks)[:stride] for _ in range(n_seq)]).astype(np.uint16)
+    limits = rng.integers(1, stride * bt + 1, size=n_seq).astype(np.int32)
+    limits[0], limits[1] = 1, stride * bt
+    q = rng.standard_normal((n_seq, n_head * D)).astype(np.float32)
+    n_ctx = stride * bt
+    scale = 1.0 / np.sqrt(D)
+    want = np.stack([oracle.compute_attention_f16(q[s], kc, vc, tables[s], bt, n_head, n_kv, D,
+                                                  int(limits[s]), n_ctx, scale)
+                     for s in range(n_seq)])
+    for threads in (1, 3, 7, 16):
+        got, secs = oracle.decode_batch_f16(q, kc, vc, tables, limits, bt, n_head, n_kv, D, n_ctx,
+                                            scale, threads)
+        assert secs >= 0.0
+        assert got.shape == want.shape
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
