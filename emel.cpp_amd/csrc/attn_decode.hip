@@ -1068,3 +1068,69 @@ extern "C" emel_error_type emelk_attn_decode_append(
   return decode_impl(g, k_pool, v_pool, layer, q, out, n_seq, kv_lens, max_kv_len, block_tables,
                      table_stride, scale, workspace, workspace_bytes, stream, k_rows, v_rows);
 }
+
+// ---- allocation-free variant -----------------------------------------------
+// The split partials live in a file-scope device array instead of a caller
+// workspace.  Each GPU the library runs on holds its own copy (sized
+// EMELK_DECODE_STATIC_SCRATCH_BYTES) until the process ends.  In host code
+// `scratch` names a host-side stand-in, never a device address: the address
+// of this device's copy comes from hipGetSymbolAddress, looked up once per
+// device with that device current, and only that address is handed to
+// kernels.  Nothing in the partials must start at zero (every split a
+// combine reads was written by this call's decode launch), so no clearing
+// runs.  Calls that overlap on one GPU share the array and race.
+namespace {
+
+static __device__ __align__(256) uint8_t scratch[EMELK_DECODE_STATIC_SCRATCH_BYTES];
+
+constexpr int k_max_devices = 64;
+std::atomic<void *> scratch_ptr[k_max_devices];
+
+// This device's copy of `scratch` (nullptr with *err set on failure).
+void *device_scratch(emel_error_type *err) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= k_max_devices) {
+    *err = EMELK_ERR_BACKEND;
+    return nullptr;
+  }
+  void *p = scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    // racing first calls on one device look up the same address
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) {
+      *err = EMELK_ERR_BACKEND;
+      return nullptr;
+    }
+    scratch_ptr[dev].store(p, std::memory_order_release);
+  }
+  return p;
+}
+
+}  // namespace
+
+extern "C" emel_error_type emelk_attn_decode_noalloc(
+    const emelk_kv_geometry *g, void *k_pool, void *v_pool, int32_t layer, const float *k_rows,
+    const float *v_rows, const float *q, float *out, int32_t n_seq, const int32_t *kv_lens,
+    int32_t max_kv_len, const uint16_t *block_tables, int32_t table_stride, float scale,
+    void *stream) {
+  emelk::pool_layout L;
+  if (emelk::make_pool_layout(g, L) != EMELK_ERR_NONE || n_seq <= 0 || n_seq > 65535 ||
+      max_kv_len <= 0 || ((k_rows == nullptr) != (v_rows == nullptr))) {
+    return EMELK_ERR_INVALID_REQUEST;
+  }
+  // the exact need of this call, checked before the device is touched
+  if (emelk::plan_decode(L, n_seq, max_kv_len).workspace_bytes > EMELK_DECODE_STATIC_SCRATCH_BYTES) {
+    return EMELK_ERR_OUT_OF_MEMORY;
+  }
+  // decode_impl's remaining argument checks, also before the device is touched
+  if (k_pool == nullptr || v_pool == nullptr || q == nullptr || out == nullptr ||
+      kv_lens == nullptr || block_tables == nullptr || layer < 0 || layer >= L.n_layer ||
+      table_stride <= 0 || !(scale > 0.0f) || !std::isfinite(scale)) {
+    return EMELK_ERR_INVALID_REQUEST;
+  }
+  emel_error_type err = EMELK_ERR_NONE;
+  void *ws = device_scratch(&err);
+  if (ws == nullptr) return err;
+  return decode_impl(g, k_pool, v_pool, layer, q, out, n_seq, kv_lens, max_kv_len, block_tables,
+                     table_stride, scale, ws, EMELK_DECODE_STATIC_SCRATCH_BYTES, stream, k_rows,
+                     v_rows);
+}

@@ -221,6 +221,9 @@ _SIGNATURES = [
     ("emelk_attn_decode_append", ctypes.c_uint32,
      [ctypes.POINTER(Geometry), _P, _P, ctypes.c_int32, _P, _P, _P, _P, ctypes.c_int32, _P,
       ctypes.c_int32, _P, ctypes.c_int32, ctypes.c_float, _P, ctypes.c_uint64, _P]),
+    ("emelk_attn_decode_noalloc", ctypes.c_uint32,
+     [ctypes.POINTER(Geometry), _P, _P, ctypes.c_int32, _P, _P, _P, _P, ctypes.c_int32, _P,
+      ctypes.c_int32, _P, ctypes.c_int32, ctypes.c_float, _P]),
     ("emelk_attn_prefill_chunk", ctypes.c_uint32,
      [ctypes.POINTER(Geometry), _P, _P, ctypes.c_int32, _P, _P, ctypes.c_int32, ctypes.c_int32,
       _P, _P, ctypes.c_int32, ctypes.c_float, _P]),

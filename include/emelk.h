@@ -283,6 +283,25 @@ emel_error_type emelk_attn_decode_append(const emelk_kv_geometry *g, void *k_poo
                                          float scale, void *workspace, uint64_t workspace_bytes,
                                          void *stream);
 
+/* Allocation-free decode.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same results as
+ * emelk_attn_decode (k_rows == v_rows == NULL) or emelk_attn_decode_append
+ * (both non-NULL), with the split partials in a static device array of
+ * EMELK_DECODE_STATIC_SCRATCH_BYTES per GPU instead of a caller workspace;
+ * it calls no allocating routine.  A call whose exact need
+ * (emelk_attn_decode_plan's bytes_out) exceeds that size returns
+ * EMELK_ERR_OUT_OF_MEMORY before touching the device.  Every call on one
+ * GPU uses that GPU's one array: calls that overlap on one GPU (other
+ * streams, other threads) race. */
+#define EMELK_DECODE_STATIC_SCRATCH_BYTES (16u << 20)
+emel_error_type emelk_attn_decode_noalloc(const emelk_kv_geometry *g, void *k_pool, void *v_pool,
+                                          int32_t layer, const float *k_rows, const float *v_rows,
+                                          const float *q, float *out, int32_t n_seq,
+                                          const int32_t *kv_lens, int32_t max_kv_len,
+                                          const uint16_t *block_tables, int32_t table_stride,
+                                          float scale, void *stream);
+
 /* Chunked-prefill attention for one layer: q fp32
  * [n_seq][n_q][n_head][head_dim]; row r of sequence s attends causally to
  * logical positions [0, q_start[s] + r] (the chunk must already be appended).
