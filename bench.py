@@ -17,6 +17,13 @@ attention must read per step / step time.  The roofline object covers the
 dominant kernel (split-K decode attention), timed with HIP events on the
 stream it runs on.  The CPU baseline is the oracle's restatement of the
 reference's paged decode route, timed on this host on a bounded sample.
+
+With no --config, the same run also measures the other BASELINE configs
+under the same clock and reports them in a "configs" object of the one JSON
+line: config 4 (q8_0 decode, B=32, ctx 16k), config 5 (chunked prefill on
+MFMA + eviction/compaction, f16 and q8_0 pools), config 2 (Llama-3.2-1B
+ragged decode) and config 1 (Qwen3-0.6B contiguous decode), each with its
+roofline, a parity sample and a bounded CPU baseline.
 """
 from __future__ import annotations
 
@@ -40,7 +47,7 @@ HBM_PEAK_GBS = 8000.0
 # profiles/ file of each workload, each scaled by the same counter's reading
 # on a plain 1 GiB copy (bench.py --copy-calibration): FETCH_SIZE x2.000,
 # WRITE_SIZE x1.000.
-PMC_TRAFFIC_BYTES = {
+PMC_TRAFFIC_BYTES = {  # workload -> bytes; source: profiles/<kernel>_<workload>.md
     "llama3-8b-b64-ctx8k": 2157387464,
     "llama3-8b-q8_0-b32-ctx16k": 1155282739,
     "llama3-8b-prefill512-evict25": 285551820,
@@ -68,7 +75,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="llama3-8b-b64-ctx8k",
+    ap.add_argument("--config", default=None,
                     choices=sorted(CONFIGS) + ["llama3-8b-prefill512-evict25",
                                                "llama3-8b-q8_0-prefill512-evict25",
                                                "gemma4-d256-prefill512-evict25",
@@ -76,6 +83,12 @@ def main():
                                                "gemma4-d512-prefill512-evict25",
                                                "llama3-8b-b64-ctx8k-generator"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="with no --config: measure config 3 only (no 'configs' object)")
+    ap.add_argument("--cpu-budget", type=float, default=10.0,
+                    help="seconds of CPU-baseline work for the headline config")
+    ap.add_argument("--no-kernel-split", action="store_true",
+                    help="skip the per-kernel durations from torch.profiler")
     ap.add_argument("--separate-append", action="store_true",
                     help="append with emelk_kv_append, then emelk_attn_decode (two launches per "
                          "layer) instead of emelk_attn_decode_append")
@@ -105,12 +118,116 @@ def main():
         return
     import emelk
 
-    if args.config in ("llama3-8b-prefill512-evict25", "llama3-8b-q8_0-prefill512-evict25",
-                       "gemma4-d256-prefill512-evict25", "gemma4-d256-q8_0-prefill512-evict25",
-                       "gemma4-d512-prefill512-evict25"):
+    if args.config is None:
+        args.config = "llama3-8b-b64-ctx8k"
+        result = run_config(args, torch, emelk, dev)
+        if not args.headline_only:
+            result["configs"] = other_configs(args, torch, emelk, dev)
+        print(json.dumps(result), flush=True)
+        return
+    print(json.dumps(run_config(args, torch, emelk, dev)), flush=True)
+
+
+PREFILL_CONFIGS = ("llama3-8b-prefill512-evict25", "llama3-8b-q8_0-prefill512-evict25",
+                   "gemma4-d256-prefill512-evict25", "gemma4-d256-q8_0-prefill512-evict25",
+                   "gemma4-d512-prefill512-evict25")
+
+# The other BASELINE configs in the default run: (label, workload, steps, warmup)
+SUB_CONFIGS = [
+    ("config4_q8_0_decode", "llama3-8b-q8_0-b32-ctx16k", 10, 2),
+    ("config5_prefill_evict_f16", "llama3-8b-prefill512-evict25", 3, 1),
+    ("config5_prefill_evict_q8_0", "llama3-8b-q8_0-prefill512-evict25", 3, 1),
+    ("config2_llama1b_ragged", "llama3.2-1b-b16-ctx1k-4k", 20, 3),
+    ("config1_qwen3_contiguous", "qwen3-0.6b-b1-ctx512", 20, 3),
+]
+SUB_KEYS = ("metric", "value", "unit", "ms_per_step", "steps", "warmup", "steps_per_s",
+            "step_launch", "dtype", "kv_type", "config", "roofline", "kernel_split",
+            "cpu_baseline", "parity_full_size", "parity_sample", "compaction")
+
+
+def other_configs(args, torch, emelk, dev):
+    out = {}
+    for label, workload, steps, warmup in SUB_CONFIGS:
+        sub = argparse.Namespace(**vars(args))
+        sub.config, sub.steps, sub.warmup = workload, steps, warmup
+        sub.cpu_budget = 3.0
+        torch.cuda.empty_cache()
+        log(f"[bench] sub-config {label} ({workload})")
+        r = run_config(sub, torch, emelk, dev)
+        out[label] = {k: r[k] for k in SUB_KEYS if k in r}
+    torch.cuda.empty_cache()
+    return out
+
+
+def gpu_head_start(torch, cycles=40_000_000):
+    """Queue a spin kernel (tens of ms) ahead of an event-timed step, so the
+    host has enqueued the step's launches before the GPU reaches them: each
+    event interval then holds GPU time only, never host launch overhead."""
+    try:
+        torch.cuda._sleep(cycles)
+    except Exception:  # absent in some builds: intervals may then hold host gaps
+        pass
+
+
+def cpu_info(threads):
+    """Provenance of a CPU-baseline figure: the threads used and the host."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = None
+    return {"cores": threads, "cpu_model": model, "nproc": os.cpu_count(),
+            "usable_cpus": usable}
+
+
+def kernel_split(args, torch, fn, names):
+    """Average device time per launch (ms) of each named kernel over one
+    eager call of fn, from torch.profiler's device trace (outside the timed
+    region).  Lets the line report the dominant kernel apart from its
+    helpers (e.g. decode_kernel vs combine_kernel)."""
+    if args.no_kernel_split:
+        return None
+    try:
+        from torch.profiler import ProfilerActivity, profile
+        torch.cuda.synchronize()
+        with profile(activities=[ProfilerActivity.CUDA]) as prof:
+            fn()
+            torch.cuda.synchronize()
+        res = {}
+        for ev in prof.key_averages():
+            for n in names:
+                if n + "<" in ev.key or ev.key.endswith(n):
+                    total = getattr(ev, "device_time_total", None)
+                    if total is None:
+                        total = getattr(ev, "cuda_time_total", 0.0)
+                    r = res.setdefault(n, {"launches": 0, "total_us": 0.0})
+                    r["launches"] += int(ev.count)
+                    r["total_us"] += float(total)
+        return {n: {"launches": r["launches"],
+                    "avg_ms": round(r["total_us"] / max(1, r["launches"]) / 1e3, 5)}
+                for n, r in res.items()} or None
+    except Exception as e:  # the profiler is a reporting aid, never a gate
+        log(f"[bench] kernel split unavailable: {e!r}")
+        return None
+
+
+def run_config(args, torch, emelk, dev):
+    if args.config in PREFILL_CONFIGS:
         return prefill_evict(args, torch, emelk, dev)
     if args.config == "llama3-8b-b64-ctx8k-generator":
         return generator(args, torch, emelk, dev)
+    return decode_run(args, torch, emelk, dev)
+
+
+def decode_run(args, torch, emelk, dev):
     L, H, HK, D, BT, B, CTX, kvt = CONFIGS[args.config]
     kv_type = emelk.KV_F16 if kvt == "f16" else emelk.KV_Q8_0
     rng = np.random.default_rng(args.seed)
@@ -220,9 +337,13 @@ def main():
     torch.cuda.synchronize()
     t_start = time.perf_counter()
     for k in range(K):
-        step(ev[k])
+        step()
     torch.cuda.synchronize()
     eager_ms = 1e3 * (time.perf_counter() - t_start) / K
+    for k in range(K):
+        gpu_head_start(torch)
+        step(ev[k])
+    torch.cuda.synchronize()
     attn_ms = [e[0].elapsed_time(e[1]) for row in ev for e in row]
     attn_avg_ms = float(np.mean(attn_ms))
 
@@ -265,70 +386,91 @@ def main():
     kv_gbs = step_kv_bytes / (ms_per_step * 1e-3) / 1e9
     achieved = kernel_bytes / (attn_avg_ms * 1e-3) / 1e9
 
-    # ---- full-size parity spot check on layer 0 + CPU baseline ----
+    split = kernel_split(args, torch, step, ["decode_kernel", "combine_kernel", "append_f16_kernel",
+                                             "append_q8_0_kernel"])
+
+    # ---- full-size parity check + CPU baseline ----
+    # f16: the oracle's restatement of compute_attention over every sequence
+    # of whole layers, on host threads, layer after layer until the CPU
+    # budget is spent; every layer's GPU output of the last step is checked.
+    # q8_0: the oracle's q8_0 route, one thread, sequence after sequence of
+    # layer 0 until the budget is spent.
     parity = None
     cpu = None
     if not args.no_cpu_baseline and kv_type == emelk.KV_F16:
         import oracle
         nthreads = args.cpu_threads or min(16, os.cpu_count() or 1)
-        layer = 0
         lb = pool_bytes // L
-        kp = k_pool[layer * lb:(layer + 1) * lb].cpu().numpy().view(np.uint16)
-        vp = v_pool[layer * lb:(layer + 1) * lb].cpu().numpy().view(np.uint16)
-        # pool [page][kv_head][t][D] -> reference token-major [page*bt + t][kv_head*D]
-        kc = np.ascontiguousarray(kp.reshape(max_blocks, HK, BT, D).transpose(0, 2, 1, 3)
-                                  ).reshape(max_blocks * BT, HK * D)
-        vc = np.ascontiguousarray(vp.reshape(max_blocks, HK, BT, D).transpose(0, 2, 1, 3)
-                                  ).reshape(max_blocks * BT, HK * D)
-        del kp, vp
-        qh = q[layer].view(B, H * D).cpu().numpy()
-        want, secs = oracle.decode_batch_f16(qh, kc, vc, tables_h, lens, BT, H, HK, D,
-                                             int(lens.max()), scale, nthreads)
-        got = out[layer].view(B, H * D).cpu().numpy()
-        err = np.abs(got.astype(np.float64) - want)
-        within = bool(np.all(err <= 2e-3 + 1e-2 * np.abs(want)))
-        parity = {"layer": layer, "sequences": B, "max_abs_err": float(err.max()),
+        worst, within, secs, layers_done = 0.0, True, 0.0, 0
+        for layer in range(L):
+            kp = k_pool[layer * lb:(layer + 1) * lb].cpu().numpy().view(np.uint16)
+            vp = v_pool[layer * lb:(layer + 1) * lb].cpu().numpy().view(np.uint16)
+            # pool [page][kv_head][t][D] -> reference token-major [page*bt + t][kv_head*D]
+            kc = np.ascontiguousarray(kp.reshape(max_blocks, HK, BT, D).transpose(0, 2, 1, 3)
+                                      ).reshape(max_blocks * BT, HK * D)
+            vc = np.ascontiguousarray(vp.reshape(max_blocks, HK, BT, D).transpose(0, 2, 1, 3)
+                                      ).reshape(max_blocks * BT, HK * D)
+            del kp, vp
+            qh = q[layer].view(B, H * D).cpu().numpy()
+            want, t_layer = oracle.decode_batch_f16(qh, kc, vc, tables_h, lens, BT, H, HK, D,
+                                                    int(lens.max()), scale, nthreads)
+            del kc, vc
+            got = out[layer].view(B, H * D).cpu().numpy()
+            err = np.abs(got.astype(np.float64) - want)
+            worst = max(worst, float(err.max()))
+            within = within and bool(np.all(err <= 2e-3 + 1e-2 * np.abs(want)))
+            secs += t_layer
+            layers_done += 1
+            if secs >= args.cpu_budget:
+                break
+        parity = {"layers": layers_done, "sequences": B, "max_abs_err": worst,
                   "within_tolerance": within}
-        cpu_step_s = secs * L  # sample = 1 layer x all sequences; scaled to L layers
+        cpu_step_s = secs / layers_done * L  # sample = whole layers; scaled to L layers
         cpu = {"value": round(step_kv_bytes / cpu_step_s / 1e9, 4), "unit": "GB/s",
-               "cores": nthreads, "kind": "port",
-               "sample": f"1 layer x {B} sequences of the same step ({secs:.2f}s wall), "
-                         f"extrapolated x{L} layers; oracle restatement of compute_attention, "
-                         f"{nthreads} threads",
-               "steps_per_s": round(1.0 / cpu_step_s, 5)}
+               **cpu_info(nthreads), "kind": "port",
+               "sample": f"{layers_done} layer(s) x {B} sequences of the same step "
+                         f"({secs:.2f}s wall), scaled to {L} layers; oracle restatement of "
+                         f"compute_attention, {nthreads} threads",
+               "steps_per_s": round(1.0 / cpu_step_s, 6)}
     elif not args.no_cpu_baseline:
-        # q8_0: the oracle's q8_0 route (dequantize_row_q8_0 values, the
-        # same softmax and fp16 probabilities as the f16 route) on a seeded
-        # sample of sequences of layer 0, one thread
         import oracle
         layer = 0
         kc, vc = (pool_token_major(p_, layer, L, max_blocks, HK, BT, D, True, oracle)
                   for p_ in (k_pool, v_pool))
-        pick = sorted(np.random.default_rng(args.seed + 1).choice(B, size=min(4, B),
-                                                                  replace=False).tolist())
+        order = np.random.default_rng(args.seed + 1).permutation(B).tolist()
         qh = q[layer].view(B, H * D).cpu().numpy()
         got = out[layer].view(B, H * D).cpu().numpy()
-        errs, t_cpu = [], 0.0
-        for s in pick:
+        errs, t_cpu, pick = [], 0.0, []
+        for s in order:
             t1 = time.perf_counter()
             want = oracle.compute_attention_q8_0(qh[s], kc, vc, tables_h[s], BT, H, HK, D,
                                                  int(lens[s]), int(lens[s]), scale)
             t_cpu += time.perf_counter() - t1
+            pick.append(s)
             errs.append((np.abs(got[s].astype(np.float64) - want),
                          2e-3 + 1e-2 * np.abs(want.astype(np.float64))))
-        parity = {"layer": layer, "sequences": pick,
+            if t_cpu >= args.cpu_budget:
+                break
+        del kc, vc
+        parity = {"layer": layer, "n_sequences": len(pick), "sequences": sorted(pick)[:16],
                   "max_abs_err": float(max(e.max() for e, _ in errs)),
                   "within_tolerance": bool(all(np.all(e <= tol) for e, tol in errs))}
-        cpu_step_s = t_cpu / len(pick) * B * L
-        cpu = {"value": round(step_kv_bytes / cpu_step_s / 1e9, 4), "unit": "GB/s", "cores": 1,
-               "kind": "port",
+        kv_done = float(sum(int(lens[s]) for s in pick))
+        cpu_step_s = t_cpu / kv_done * float(lens.sum()) * L  # per attended token, scaled
+        cpu = {"value": round(step_kv_bytes / cpu_step_s / 1e9, 4), "unit": "GB/s",
+               **cpu_info(1), "kind": "port",
                "sample": f"{len(pick)} sequences x 1 layer of the step ({t_cpu:.2f}s), "
-                         f"extrapolated to {B} sequences x {L} layers; oracle q8_0 route, "
-                         "1 thread",
+                         f"scaled by attended tokens to {B} sequences x {L} layers; oracle q8_0 "
+                         "route, 1 thread",
                "steps_per_s": round(1.0 / cpu_step_s, 6)}
 
+    metric = ("KV-read HBM GB/s (% of peak) + decode steps/s, 8B-shape b64 ctx8k"
+              if args.config == "llama3-8b-b64-ctx8k" else
+              f"KV-read HBM GB/s (% of peak) + decode steps/s, {args.config}")
+    traffic = None if args.separate_append else PMC_TRAFFIC_BYTES.get(args.config)
+    dk = (split or {}).get("decode_kernel")
     result = {
-        "metric": "KV-read HBM GB/s (% of peak) + decode steps/s, 8B-shape b64 ctx8k",
+        "metric": metric,
         "value": round(kv_gbs, 2),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -350,17 +492,27 @@ def main():
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": (None if args.separate_append
-                                 else PMC_TRAFFIC_BYTES.get(args.config)),
+                     "traffic": traffic,
+                     "traffic_source": (f"profiles/decode_kernel_{args.config}.md (rocprofv3 "
+                                        "--pmc FETCH_SIZE / WRITE_SIZE of an earlier run of this "
+                                        "workload, copy-calibrated)") if traffic else None,
                      "kernel": ("decode_kernel + combine_kernel (HIP events per layer call)"
                                 if args.separate_append else
                                 "decode_kernel with the fused append + combine_kernel (HIP events "
                                 "per layer call)"),
-                     "bytes_per_launch": kernel_bytes, "avg_launch_ms": round(attn_avg_ms, 4)},
+                     "bytes_per_launch": kernel_bytes, "avg_launch_ms": round(attn_avg_ms, 4),
+                     "decode_kernel_only": ({
+                         "avg_launch_ms": dk["avg_ms"],
+                         "achieved": round(kernel_bytes / (dk["avg_ms"] * 1e-3) / 1e9, 2),
+                         "frac": round(kernel_bytes / (dk["avg_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                                       4),
+                         "source": "torch.profiler device trace of one eager step"}
+                         if dk else None)},
+        "kernel_split": split,
         "cpu_baseline": cpu,
         "parity_full_size": parity,
     }
-    print(json.dumps(result), flush=True)
+    return result
 
 
 def pool_token_major(pool, layer, n_layer, max_blocks, n_kv, bt, d, q8, oracle):
@@ -459,9 +611,13 @@ def prefill_evict(args, torch, emelk, dev):
            for _ in range(L)] for _ in range(K)]
     t0 = time.perf_counter()
     for k in range(K):
-        step(ev[k])
+        step()
     torch.cuda.synchronize()
     ms_step = 1e3 * (time.perf_counter() - t0) / K
+    for k in range(K):
+        gpu_head_start(torch)
+        step(ev[k])
+    torch.cuda.synchronize()
     attn_ms = float(np.mean([e[0].elapsed_time(e[1]) for row in ev for e in row]))
     # bytes the kernel must move per launch: the unique K/V of the layer
     # (prefix + chunk, every KV head), the fp32 queries and the fp32 output
@@ -483,11 +639,17 @@ def prefill_evict(args, torch, emelk, dev):
         tables_h = tables.cpu().numpy().view(np.uint16)
         route = oracle.compute_attention_q8_0 if q8 else oracle.compute_attention_f16
         prng = np.random.default_rng(args.seed + 2)
-        pick = [(int(prng.integers(B)), int(prng.integers(NQ))) for _ in range(4)]
         qh = q[layer].cpu().numpy()
         got = out.cpu().numpy()
-        worst, ok_all, t_cpu, keys = 0.0, True, 0.0, 0
-        for s_, r_ in pick:
+        worst, ok_all, t_cpu, keys, pick = 0.0, True, 0.0, 0, []
+        # seeded (sequence, row) pairs, the chunk's first and last rows
+        # first, until the CPU budget is spent (at least 4)
+        cand = [(0, 0), (B - 1, NQ - 1)] + [(int(prng.integers(B)), int(prng.integers(NQ)))
+                                            for _ in range(4096)]
+        for s_, r_ in cand:
+            if len(pick) >= 4 and t_cpu >= args.cpu_budget:
+                break
+            pick.append((s_, r_))
             lim = P0 + r_ + 1
             t1 = time.perf_counter()
             want = route(qh[s_, r_].ravel(), kc, vc, tables_h[s_], BT, H, HK, D, lim, lim, scale)
@@ -496,15 +658,19 @@ def prefill_evict(args, torch, emelk, dev):
             e = np.abs(got[s_, r_].ravel().astype(np.float64) - want)
             worst = max(worst, float(e.max()))
             ok_all = ok_all and bool(np.all(e <= 2e-3 + 1e-2 * np.abs(want)))
-        parity = {"layer": layer, "rows": pick, "max_abs_err": worst, "within_tolerance": ok_all}
+        parity = {"layer": layer, "n_rows": len(pick), "first_rows": pick[:6],
+                  "max_abs_err": worst, "within_tolerance": ok_all}
         # the per-row route's time per attended key, scaled to a layer's keys
         layer_keys = B * float(np.sum(P0 + rows + 1))
         cpu_layer_s = t_cpu / keys * layer_keys
-        cpu = {"value": round(flops_layer / cpu_layer_s / 1e12, 6), "unit": "TFLOP/s", "cores": 1,
-               "kind": "port",
+        cpu = {"value": round(flops_layer / cpu_layer_s / 1e12, 6), "unit": "TFLOP/s",
+               **cpu_info(1), "kind": "port",
                "sample": f"{len(pick)} rows of layer {layer} ({t_cpu:.2f}s), scaled by attended "
-                         "keys to the layer's 4096 rows; oracle per-row route, 1 thread"}
+                         f"keys to the layer's {B * NQ} rows; oracle per-row route, 1 thread"}
         del kc, vc
+
+    split = kernel_split(args, torch, step, ["prefill_kernel", "append_f16_kernel",
+                                             "append_q8_0_kernel", "decode_kernel"])
 
     # eviction + compaction
     evicted = 0
@@ -524,6 +690,7 @@ def prefill_evict(args, torch, emelk, dev):
     torch.cuda.synchronize()
     copy_ms = e0.elapsed_time(e1)
     copy_bytes = 2 * 2 * len(moves) * L * page_bytes  # read + write, K and V
+    traffic = PMC_TRAFFIC_BYTES.get(args.config)
     res = {
         "metric": "chunked-prefill attention TFLOP/s (MFMA f16, fp32 acc) + compaction GB/s",
         "kv_type": "q8_0" if q8 else "f16",
@@ -534,17 +701,26 @@ def prefill_evict(args, torch, emelk, dev):
                    "chunk": NQ, "n_layer": L, "block_tokens": BT},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": 2500.0,
                      "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4),
-                     "traffic": PMC_TRAFFIC_BYTES.get(args.config),
+                     "traffic": traffic,
+                     "traffic_source": (f"profiles/prefill_kernel_{args.config}.md (rocprofv3 "
+                                        "--pmc FETCH_SIZE / WRITE_SIZE of an earlier run of this "
+                                        "workload, copy-calibrated)") if traffic else None,
                      "algorithmic_bytes": prefill_bytes,
                      "kernel": "prefill_kernel (HIP events per layer call)",
                      "flops_per_launch": flops_layer, "avg_launch_ms": round(attn_ms, 4)},
+        "kernel_split": split,
         "cpu_baseline": cpu,
         "parity_sample": parity,
         "compaction": {"pages_evicted": evicted, "moves": len(moves), "ms": round(copy_ms, 4),
                        "GB/s": round(copy_bytes / (copy_ms * 1e-3) / 1e9, 1),
-                       "bytes": copy_bytes},
+                       "bytes": copy_bytes,
+                       "roofline": {"bound": "hbm", "kernel": "copy_blocks_kernel (HIP events)",
+                                    "achieved": round(copy_bytes / (copy_ms * 1e-3) / 1e9, 1),
+                                    "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                    "frac": round(copy_bytes / (copy_ms * 1e-3) / 1e9
+                                                  / HBM_PEAK_GBS, 4)}},
     }
-    print(json.dumps(res), flush=True)
+    return res
 
 
 def generator(args, torch, emelk, dev):
@@ -645,7 +821,7 @@ def generator(args, torch, emelk, dev):
         "eager_ms_per_step": round(eager_ms, 4),
     }
     dec.close()
-    print(json.dumps(res), flush=True)
+    return res
 
 
 if __name__ == "__main__":
