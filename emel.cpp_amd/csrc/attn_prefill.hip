@@ -41,6 +41,9 @@ using namespace emelk::dev;
 constexpr int k_sub = 32;   // keys per MFMA sub-tile (one score accumulator)
 constexpr float k_rescale = 8.0f;  // lazy-rescale threshold (log2 units)
 constexpr int k_max_seq_pages = EMELK_MAX_BLOCKS_PER_SEQUENCE;  // LDS page list
+// word 3 of a raw buffer resource (gfx9 family): 32-bit data format, no
+// swizzle, offsets checked against num_records
+constexpr int k_rsrc_word3 = 0x00020000;
 
 typedef _Float16 half8_v __attribute__((ext_vector_type(8)));
 typedef float float16_v __attribute__((ext_vector_type(16)));
@@ -284,6 +287,7 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
   // get zero V (their P is 0, and 0 * garbage could be NaN); a sub-tile on an
   // invalid page is all zeros, as the general path gives.
   const bool uniform_tiles = bt_shift >= 5;
+  constexpr bool BUF = !Q8 && NT == 4 * D && KI == NS && VI == NS;
   // Offsets inside a 32-key sub-tile (q8_0: of the values, and of the
   // scale of the item's 32-value block from the scale plane).
   uint32_t kofs[KI], vofs[VI], ksofs[KI], vsofs[VI];
@@ -306,8 +310,80 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
     vofs[i] = static_cast<uint32_t>(key % k_sub) * ROWB + dp * (ROWB / (D / 2));
     vsofs[i] = static_cast<uint32_t>(key % k_sub) * SROWB + (dp / 16) * 2;
   }
+  // Page of each sub-tile of tile t (0xFFFF: invalid or past the end).
+  auto tile_pages = [&](int t, uint32_t (&pg)[NS]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+      const int kj = t * KT + j * k_sub;
+      const int lb = kj >> bt_shift;
+      pg[j] = (kj < total && lb < n_pt) ? static_cast<uint32_t>(s_ptab[lb]) : 0xFFFFu;
+    }
+  };
+  // The BUF path reads the next tile's page ids one tile ahead, so the
+  // LDS round trip of the lookup never sits between a tile's start and its
+  // loads.
+  uint32_t pg_next[NS];
   auto load_tile_uniform = [&](int t, stage_t &R) __attribute__((always_inline)) {
     const int key0 = t * KT;
+    if constexpr (BUF) {
+      // f16, one staging item of K and of V per thread and sub-tile (NT =
+      // 4 * D): item i of every thread lies in sub-tile i.  One buffer
+      // resource per sub-tile and pool, based at the sub-tile's first key
+      // row (wave-uniform, built on the scalar unit), so each load is that
+      // base + a fixed per-thread offset.  An invalid page gets a resource
+      // of 0 bytes: its loads return zeros.
+      __amdgpu_buffer_rsrc_t krs[NS], vrs[NS];
+      bool all_valid = true;
+      uint32_t pg[NS];
+      if (t == 0) {
+        tile_pages(0, pg);
+      } else {
+#pragma unroll
+        for (int j = 0; j < NS; ++j) pg[j] = pg_next[j];
+      }
+      tile_pages(t + 1, pg_next);
+#pragma unroll
+      for (int j = 0; j < NS; ++j) {
+        const int kj = key0 + j * k_sub;
+        const uint32_t page = __builtin_amdgcn_readfirstlane(pg[j]);
+        const bool valid = page != 0xFFFFu;
+        all_valid = all_valid && valid;
+        const uint64_t off = layer_base + static_cast<uint64_t>(valid ? page : 0u) * P.L.page_bytes +
+                             static_cast<uint64_t>(kj & (bt - 1)) * ROWB;
+        const int bytes = valid ? static_cast<int>(k_sub * ROWB) : 0;
+        krs[j] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(P.k_pool + off), 0, bytes,
+                                                   k_rsrc_word3);
+        vrs[j] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(P.v_pool + off), 0, bytes,
+                                                   k_rsrc_word3);
+      }
+#pragma unroll
+      for (int i = 0; i < KI; ++i) {
+        if (KITEMS % NT == 0 || tid + i * NT < KITEMS) {
+          const auto v = __builtin_amdgcn_raw_buffer_load_b128(krs[i], static_cast<int>(kofs[i]), 0, 0);
+          R.rk[i] = uint4_t{v[0], v[1], v[2], v[3]};
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < VI; ++i) {
+        if (VITEMS % NT == 0 || tid + i * NT < VITEMS) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            R.rv[i][e] = __builtin_amdgcn_raw_buffer_load_b32(
+                vrs[i], static_cast<int>(vofs[i] + e * ROWB), 0, 0);
+          }
+        }
+      }
+      (void)all_valid;
+      if (key0 + KT > total) {  // keys past the end: zero V (P is 0 there; 0 * NaN is not)
+#pragma unroll
+        for (int i = 0; i < VI; ++i) {
+          const int k4 = key0 + 4 * ((tid + i * NT) / (D / 2));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) R.rv[i][e] = k4 + e < total ? R.rv[i][e] : 0u;
+        }
+      }
+      return;
+    }
     uint64_t base[NS], sbase[NS];  // values, and (q8_0) scales, of each sub-tile's first key
     bool valid[NS];
 #pragma unroll
@@ -492,13 +568,15 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
         // 4.5M per launch at the Llama-3-8B chunk shape)
         const bool odd_first = (tid & 8) != 0;
         const int r0 = 2 * dp + (odd_first ? 1 : 0);
+        // the row written first takes the high halves when it is the odd
+        // row: chosen by the permute selector, not by selecting data
+        const uint32_t sel_first = odd_first ? 0x07060302u : 0x05040100u;
+        const uint32_t sel_second = odd_first ? 0x05040100u : 0x07060302u;
         auto put = [&](uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3, int plane) {
-          const uint32_t lo01 = __builtin_amdgcn_perm(w1, w0, 0x05040100u);
-          const uint32_t lo23 = __builtin_amdgcn_perm(w3, w2, 0x05040100u);
-          const uint32_t hi01 = __builtin_amdgcn_perm(w1, w0, 0x07060302u);
-          const uint32_t hi23 = __builtin_amdgcn_perm(w3, w2, 0x07060302u);
-          const uint2 first = odd_first ? uint2{hi01, hi23} : uint2{lo01, lo23};
-          const uint2 second = odd_first ? uint2{lo01, lo23} : uint2{hi01, hi23};
+          const uint2 first{__builtin_amdgcn_perm(w1, w0, sel_first),
+                            __builtin_amdgcn_perm(w3, w2, sel_first)};
+          const uint2 second{__builtin_amdgcn_perm(w1, w0, sel_second),
+                             __builtin_amdgcn_perm(w3, w2, sel_second)};
           *reinterpret_cast<uint2 *>(&s_vt[vbuf][plane][r0][slot]) = first;
           *reinterpret_cast<uint2 *>(&s_vt[vbuf][plane][r0 ^ 1][slot]) = second;
         };
@@ -539,7 +617,7 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
         }
       }
     }
-    if constexpr (NS > 1) {
+    if constexpr (NS > 1 && Q8) {
       // operand reads just ahead of their MFMAs rather than all hoisted,
       // which would need 4 * NS * KSTEPS * PL registers at once
 #pragma unroll
@@ -547,6 +625,19 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
         __builtin_amdgcn_sched_group_barrier(0x100, NS, 0);
         __builtin_amdgcn_sched_group_barrier(0x008, NS, 0);
       }
+    } else if constexpr (NS > 1) {
+      // f16: the operand reads run two k-steps ahead of their MFMAs (one
+      // step ahead left the LDS latency exposed: 3% slower at the
+      // Llama-3-8B chunk shape)
+      constexpr int LA = 2;
+      __builtin_amdgcn_sched_group_barrier(0x100, LA * NS, 0);
+#pragma unroll
+      for (int kk = 0; kk < KSTEPS - LA; ++kk) {
+        __builtin_amdgcn_sched_group_barrier(0x008, NS, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, NS, 0);
+      }
+#pragma unroll
+      for (int kk = 0; kk < LA; ++kk) __builtin_amdgcn_sched_group_barrier(0x008, NS, 0);
     }
   };
   // Max / sum of v and the value 32 lanes apart, by v_permlane32_swap: with
@@ -610,8 +701,6 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
     const float mc = m * P.c;
     float ps8[8];
 #pragma unroll
-    for (int r = 0; r < 8; ++r) ps8[r] = 0.0f;
-#pragma unroll
     for (int j = 0; j < NS; ++j) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -624,7 +713,10 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
       }
       // pairwise partial sums: short dependency chains
 #pragma unroll
-      for (int r = 0; r < 8; ++r) ps8[r] += s[j][2 * r] + s[j][2 * r + 1];
+      for (int r = 0; r < 8; ++r) {
+        const float pair = s[j][2 * r] + s[j][2 * r + 1];
+        ps8[r] = j == 0 ? pair : ps8[r] + pair;
+      }
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) ps8[r] += ps8[r + 4];
@@ -680,6 +772,20 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
           }
         }
       }
+    }
+    if constexpr (!Q8) {
+      // the V operand reads run four MFMAs ahead (measured 2% faster than
+      // the compiler's own order at the Llama-3-8B chunk shape)
+      constexpr int NPV = NS * 2 * DCH;
+      constexpr int LAP = 4;
+      __builtin_amdgcn_sched_group_barrier(0x100, LAP, 1);
+#pragma unroll
+      for (int k = 0; k < NPV - LAP; ++k) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+      }
+#pragma unroll
+      for (int k = 0; k < LAP; ++k) __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
     }
   };
 
