@@ -48,10 +48,12 @@ HBM_PEAK_GBS = 8000.0
 # on a plain 1 GiB copy (bench.py --copy-calibration): FETCH_SIZE x2.000,
 # WRITE_SIZE x1.000.
 PMC_TRAFFIC_BYTES = {  # workload -> bytes; source: profiles/<kernel>_<workload>.md
-    "llama3-8b-b64-ctx8k": 2157387464,
-    "llama3-8b-q8_0-b32-ctx16k": 1155282739,
-    "llama3-8b-prefill512-evict25": 285551820,
-    "llama3-8b-q8_0-prefill512-evict25": 214867558,
+    "llama3-8b-b64-ctx8k": 2157313173,
+    "llama3-8b-q8_0-b32-ctx16k": 1150323019,
+    "llama3-8b-prefill512-evict25": 287661314,
+    "llama3-8b-q8_0-prefill512-evict25": 214842727,
+    "llama3.2-1b-b16-ctx1k-4k": 94657232,
+    "qwen3-0.6b-b1-ctx512": 2646457,
     "gemma4-d256-prefill512-evict25": 105300848,
     "gemma4-d256-q8_0-prefill512-evict25": 87748528,
     "gemma4-d512-prefill512-evict25": 285765904,
@@ -308,44 +310,49 @@ def decode_run(args, torch, emelk, dev):
     new_k2 = [t.view(B, HK * D) for t in new_k]
     new_v2 = [t.view(B, HK * D) for t in new_v]
 
-    def step(events=None):
+    def step():
         for layer in range(L):
             if args.separate_append:
                 emelk.append(g, k_pool, v_pool, layer, new_k[layer], new_v[layer], positions,
                              tables)
-            if events is not None:
-                events[layer][0].record(stream)
-            if args.separate_append:
                 emelk.decode(g, k_pool, v_pool, layer, q[layer], out[layer], kv_lens, max_len,
                              tables, scale, ws)
             else:  # the step's store of the new token and its attention in one launch
                 emelk.decode_append(g, k_pool, v_pool, layer, new_k2[layer], new_v2[layer],
                                     q[layer], out[layer], kv_lens, max_len, tables, scale, ws)
-            if events is not None:
-                events[layer][1].record(stream)
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
 
-    # Kernel timing: eager launches with HIP events around each layer's
-    # decode call (decode_kernel, with the new token's store unless --separate-append, +
-    # combine_kernel) on the stream they run on.
+    # eager step time (host launch path included)
     K = args.steps
-    ev = [[[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)]
-           for _ in range(L)] for _ in range(K)]
     torch.cuda.synchronize()
     t_start = time.perf_counter()
     for k in range(K):
         step()
     torch.cuda.synchronize()
     eager_ms = 1e3 * (time.perf_counter() - t_start) / K
+    # Kernel timing: after a GPU head start, one HIP event pair on the
+    # kernels' stream around the L back-to-back decode calls of a step (the
+    # appends of --separate-append left out: their rows are already stored),
+    # averaged per call.  No host gap and no event packet sits between two
+    # calls, so the figure is the decode (+ combine) kernels' own time.
+    blk = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(K)]
     for k in range(K):
         gpu_head_start(torch)
-        step(ev[k])
+        blk[k][0].record(stream)
+        for layer in range(L):
+            if args.separate_append:
+                emelk.decode(g, k_pool, v_pool, layer, q[layer], out[layer], kv_lens, max_len,
+                             tables, scale, ws)
+            else:
+                emelk.decode_append(g, k_pool, v_pool, layer, new_k2[layer], new_v2[layer],
+                                    q[layer], out[layer], kv_lens, max_len, tables, scale, ws)
+        blk[k][1].record(stream)
     torch.cuda.synchronize()
-    attn_ms = [e[0].elapsed_time(e[1]) for row in ev for e in row]
-    attn_avg_ms = float(np.mean(attn_ms))
+    attn_avg_ms = float(np.mean([a.elapsed_time(b) for a, b in blk])) / L
 
     # Step timing: the 32-layer step (96 launches) captured once as a HIP
     # graph and replayed K times, as a serving loop would run it.
@@ -594,31 +601,33 @@ def prefill_evict(args, torch, emelk, dev):
     scale = float(1.0 / np.sqrt(D))
     stream = torch.cuda.current_stream()
 
-    def step(events=None):
+    def step():
         for layer in range(L):
             emelk.append(g, k_pool, v_pool, layer, ck[layer], cv[layer], qs, tables)
-            if events is not None:
-                events[layer][0].record(stream)
             emelk.prefill_chunk(g, k_pool, v_pool, layer, q[layer], out, qs, tables, scale)
-            if events is not None:
-                events[layer][1].record(stream)
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
     K = args.steps
-    ev = [[[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)]
-           for _ in range(L)] for _ in range(K)]
     t0 = time.perf_counter()
     for k in range(K):
         step()
     torch.cuda.synchronize()
     ms_step = 1e3 * (time.perf_counter() - t0) / K
+    # kernel timing: one HIP event pair around the L back-to-back chunk
+    # attention calls (the chunk rows are already appended), after a GPU
+    # head start, averaged per call
+    blk = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(K)]
     for k in range(K):
         gpu_head_start(torch)
-        step(ev[k])
+        blk[k][0].record(stream)
+        for layer in range(L):
+            emelk.prefill_chunk(g, k_pool, v_pool, layer, q[layer], out, qs, tables, scale)
+        blk[k][1].record(stream)
     torch.cuda.synchronize()
-    attn_ms = float(np.mean([e[0].elapsed_time(e[1]) for row in ev for e in row]))
+    attn_ms = float(np.mean([a.elapsed_time(b) for a, b in blk])) / L
     # bytes the kernel must move per launch: the unique K/V of the layer
     # (prefix + chunk, every KV head), the fp32 queries and the fp32 output
     prefill_bytes = (B * HK * (P0 + NQ) * (page_bytes // (HK * BT)) * 2

@@ -436,6 +436,9 @@ def _ptr(t):
 _I16 = ("int16", "uint16")
 
 
+_DTYPE_NAMES = {}
+
+
 def _is_tensor(t):
     return hasattr(t, "is_cuda") and hasattr(t, "dtype")
 
@@ -454,7 +457,9 @@ def _need(t, name, dtypes=None, shape=None, min_bytes=None, optional=False):
     if not t.is_contiguous():
         raise ValueError(f"{name}: tensor must be contiguous")
     if dtypes is not None:
-        dt = str(t.dtype).replace("torch.", "")
+        dt = _DTYPE_NAMES.get(t.dtype)
+        if dt is None:
+            dt = _DTYPE_NAMES[t.dtype] = str(t.dtype).replace("torch.", "")
         if dt not in dtypes:
             raise TypeError(f"{name}: dtype {dt}, expected {' or '.join(dtypes)}")
     if shape is not None:
@@ -466,8 +471,19 @@ def _need(t, name, dtypes=None, shape=None, min_bytes=None, optional=False):
         raise ValueError(f"{name}: {t.numel() * t.element_size()} bytes, need {min_bytes}")
 
 
+_POOL_BYTES = {}
+
+
+def _pool_bytes_cached(g):
+    key = (g.n_layer, g.n_head, g.n_head_kv, g.head_dim, g.block_tokens, g.max_blocks, g.kv_type)
+    pb = _POOL_BYTES.get(key)
+    if pb is None:
+        pb = _POOL_BYTES[key] = pool_bytes(g)
+    return pb
+
+
 def _pools(g, k_pool, v_pool):
-    pb = pool_bytes(g)
+    pb = _pool_bytes_cached(g)
     _need(k_pool, "k_pool", min_bytes=pb)
     _need(v_pool, "v_pool", min_bytes=pb)
 
