@@ -171,6 +171,29 @@ def gpu_head_start(torch, cycles=40_000_000):
         pass
 
 
+def timed_blocks(torch, stream, launch, reps):
+    """HIP event time (ms) of `launch()` (a block of back-to-back calls on
+    `stream`), `reps` times.  Each block is queued behind a spin kernel; a
+    block whose launches were not all queued before the GPU reached its
+    start event (the host stalled, e.g. freeing a large array) may hold host
+    gaps and is measured again."""
+    times, tries = [], 0
+    while len(times) < reps and tries < 4 * reps:
+        tries += 1
+        gpu_head_start(torch)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        launch()
+        e1.record(stream)
+        ahead = not e0.query()  # the GPU was still spinning when the last call was queued
+        torch.cuda.synchronize()
+        if ahead:
+            times.append(e0.elapsed_time(e1))
+    if not times:
+        raise RuntimeError("could not queue a timed block ahead of the GPU")
+    return times
+
+
 def cpu_info(threads):
     """Provenance of a CPU-baseline figure: the threads used and the host."""
     model = "unknown"
@@ -338,11 +361,7 @@ def decode_run(args, torch, emelk, dev):
     # appends of --separate-append left out: their rows are already stored),
     # averaged per call.  No host gap and no event packet sits between two
     # calls, so the figure is the decode (+ combine) kernels' own time.
-    blk = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(K)]
-    for k in range(K):
-        gpu_head_start(torch)
-        blk[k][0].record(stream)
+    def decode_block():
         for layer in range(L):
             if args.separate_append:
                 emelk.decode(g, k_pool, v_pool, layer, q[layer], out[layer], kv_lens, max_len,
@@ -350,9 +369,8 @@ def decode_run(args, torch, emelk, dev):
             else:
                 emelk.decode_append(g, k_pool, v_pool, layer, new_k2[layer], new_v2[layer],
                                     q[layer], out[layer], kv_lens, max_len, tables, scale, ws)
-        blk[k][1].record(stream)
-    torch.cuda.synchronize()
-    attn_avg_ms = float(np.mean([a.elapsed_time(b) for a, b in blk])) / L
+
+    attn_avg_ms = float(np.mean(timed_blocks(torch, stream, decode_block, K))) / L
 
     # Step timing: the 32-layer step (96 launches) captured once as a HIP
     # graph and replayed K times, as a serving loop would run it.
@@ -618,16 +636,11 @@ def prefill_evict(args, torch, emelk, dev):
     # kernel timing: one HIP event pair around the L back-to-back chunk
     # attention calls (the chunk rows are already appended), after a GPU
     # head start, averaged per call
-    blk = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(K)]
-    for k in range(K):
-        gpu_head_start(torch)
-        blk[k][0].record(stream)
+    def chunk_block():
         for layer in range(L):
             emelk.prefill_chunk(g, k_pool, v_pool, layer, q[layer], out, qs, tables, scale)
-        blk[k][1].record(stream)
-    torch.cuda.synchronize()
-    attn_ms = float(np.mean([a.elapsed_time(b) for a, b in blk])) / L
+
+    attn_ms = float(np.mean(timed_blocks(torch, stream, chunk_block, K))) / L
     # bytes the kernel must move per launch: the unique K/V of the layer
     # (prefix + chunk, every KV head), the fp32 queries and the fp32 output
     prefill_bytes = (B * HK * (P0 + NQ) * (page_bytes // (HK * BT)) * 2
