@@ -647,57 +647,90 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
       for (int i = 0; i < 16; ++i) S.acc[h][i] = fmaf(-1152.0f, S.vw[h], S.acc[h][i]);
     }
   }
-  // merge the token groups of the wave (lane bits >= log2(LPT))
+  // Merge the wave's NGW token groups (lane bits >= log2(LPT)).  Every lane
+  // first rescales its partial sums to the wave's max, so the rest is a
+  // plain sum: l is summed across the groups, and acc is reduced by halving
+  // exchanges (each round a lane sends the half of its float4 chunks its
+  // partner keeps and adds the half it keeps), so after log2(NGW) rounds
+  // each lane holds whole sums of NCH / NGW chunks instead of every lane
+  // exchanging all G * 16 values each round.
+  constexpr int NCH = G * 4;  // float4 chunks of acc: chunk c = (head c / 4, dims 4 * (c % 4))
+  constexpr int R = __builtin_ctz(NGW);
+  constexpr int RS = R < __builtin_ctz(NCH) ? R : __builtin_ctz(NCH);  // halving rounds
+  float M[G];
 #pragma unroll
-  for (int mask = LPT; mask < k_wave; mask <<= 1) {
+  for (int h = 0; h < G; ++h) {
+    M[h] = S.m[h];
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-      const float mo = wave_shfl_xor(S.m[h], mask);
-      const float lo = wave_shfl_xor(S.l[h], mask);
-      const float mn = fmaxf(S.m[h], mo);
-      const float ms = mn == -INFINITY ? 0.0f : mn;
-      const float a = fast_exp2(S.m[h] - ms);
-      const float b = fast_exp2(mo - ms);
-      S.l[h] = S.l[h] * a + lo * b;
+    for (int mask = LPT; mask < k_wave; mask <<= 1) M[h] = fmaxf(M[h], wave_shfl_xor(M[h], mask));
+    const float ms = M[h] == -INFINITY ? 0.0f : M[h];
+    const float f = fast_exp2(S.m[h] - ms);  // 0 for a lane that saw no token
+    S.l[h] *= f;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        S.acc[h][i] = S.acc[h][i] * a + wave_shfl_xor(S.acc[h][i], mask) * b;
-      }
-      S.m[h] = mn;
+    for (int i = 0; i < 16; ++i) S.acc[h][i] *= f;
+  }
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+#pragma unroll
+    for (int mask = LPT; mask < k_wave; mask <<= 1) S.l[h] += wave_shfl_xor(S.l[h], mask);
+  }
+  float (&v)[NCH * 4] = reinterpret_cast<float (&)[NCH * 4]>(S.acc);
+#pragma unroll
+  for (int r = 0; r < RS; ++r) {
+    const int n = (NCH >> r) * 4;  // floats held before this round
+    const bool upper = (grp >> r) & 1;
+#pragma unroll
+    for (int k = 0; k < n / 2; ++k) {
+      const float send = upper ? v[k] : v[k + n / 2];
+      const float keep = upper ? v[k + n / 2] : v[k];
+      v[k] = keep + wave_shfl_xor(send, LPT << r);
     }
   }
+  constexpr int HELD = (NCH >> RS) * 4;  // floats held: chunks first_chunk .. + HELD / 4
+#pragma unroll
+  for (int r = RS; r < R; ++r) {  // more groups than chunks: sum what is held
+#pragma unroll
+    for (int k = 0; k < HELD; ++k) v[k] += wave_shfl_xor(v[k], LPT << r);
+  }
+  // the chunk index a lane holds: bit r of grp picks the upper half in round r
+  int first_chunk = 0;
+#pragma unroll
+  for (int r = 0; r < RS; ++r) first_chunk += ((grp >> r) & 1) * (NCH >> (r + 1));
+  const bool writer = (grp >> RS) == 0;  // one lane group per chunk after the sum rounds
   if (P.direct_out != nullptr) {  // the only split: o = acc / l
-    if (grp == 0) {
+    if (writer) {
 #pragma unroll
-      for (int h = 0; h < G; ++h) {
-        const float inv = S.l[h] > 0.0f ? 1.0f / S.l[h] : 0.0f;
+      for (int c = 0; c < HELD / 4; ++c) {
+        const int ch = first_chunk + c;
+        const int h = ch / 4;
+        float l = S.l[0];
+#pragma unroll
+        for (int hh = 1; hh < G; ++hh) l = h == hh ? S.l[hh] : l;
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
         float *op = P.direct_out + (static_cast<uint64_t>(seq) * P.L.n_head + kvh * G + h) * D;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          *reinterpret_cast<float4_t *>(op + lane_dim<D, Q8>(lane_in_row, 4 * j)) =
-              float4_t{S.acc[h][4 * j] * inv, S.acc[h][4 * j + 1] * inv,
-                       S.acc[h][4 * j + 2] * inv, S.acc[h][4 * j + 3] * inv};
-        }
+        *reinterpret_cast<float4_t *>(op + lane_dim<D, Q8>(lane_in_row, 4 * (ch % 4))) =
+            float4_t{v[4 * c] * inv, v[4 * c + 1] * inv, v[4 * c + 2] * inv, v[4 * c + 3] * inv};
       }
     }
     return;
   }
-  if (grp == 0) {
+  if (writer) {
+#pragma unroll
+    for (int c = 0; c < HELD / 4; ++c) {
+      const int ch = first_chunk + c;
+      const uint64_t slot =
+          (static_cast<uint64_t>(seq) * P.L.n_head + kvh * G + ch / 4) * P.max_splits + split;
+      *reinterpret_cast<float4_t *>(P.part_acc + slot * D + lane_dim<D, Q8>(lane_in_row, 4 * (ch % 4))) =
+          float4_t{v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]};
+    }
+  }
+  if (lane == 0) {
 #pragma unroll
     for (int h = 0; h < G; ++h) {
       const uint64_t slot =
           (static_cast<uint64_t>(seq) * P.L.n_head + kvh * G + h) * P.max_splits + split;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        *reinterpret_cast<float4_t *>(P.part_acc + slot * D +
-                                      lane_dim<D, Q8>(lane_in_row, 4 * j)) =
-            float4_t{S.acc[h][4 * j], S.acc[h][4 * j + 1], S.acc[h][4 * j + 2],
-                     S.acc[h][4 * j + 3]};
-      }
-      if (lane_in_row == 0) {
-        P.part_ml[slot * 2] = S.m[h];
-        P.part_ml[slot * 2 + 1] = S.l[h];
-      }
+      P.part_ml[slot * 2] = M[h];
+      P.part_ml[slot * 2 + 1] = S.l[h];
     }
   }
 }
