@@ -205,7 +205,7 @@ __device__ __forceinline__ void load_row_uniform(const uint8_t *__restrict__ reg
 // (kernel/detail.hpp:804-824), the two lanes of a block sharing its amax.
 template <int D, bool Q8>
 __device__ __forceinline__ void new_row_regs(const float *__restrict__ row, int32_t lane_in_row,
-                                             row_regs<D, Q8> &r) {
+                                             int32_t block_partner, row_regs<D, Q8> &r) {
   if constexpr (!Q8) {
     const float4_t a0 = *reinterpret_cast<const float4_t *>(row + 8 * lane_in_row);
     const float4_t a1 = *reinterpret_cast<const float4_t *>(row + 8 * lane_in_row + 4);
@@ -228,7 +228,7 @@ __device__ __forceinline__ void new_row_regs(const float *__restrict__ row, int3
     float amax = 0.0f;
 #pragma unroll
     for (int j = 0; j < 16; ++j) amax = fmaxf(amax, fabsf(v[j]));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, k_wave));  // the other half of the block
+    amax = fmaxf(amax, __shfl_xor(amax, block_partner, k_wave));  // the other half of the block
     const float d = amax / 127.0f;
     const float inv_d = d != 0.0f ? 1.0f / d : 0.0f;
     uint32_t w[4] = {0u, 0u, 0u, 0u};
@@ -271,6 +271,11 @@ struct decode_state {
   float acc[G][16];
   float kbias[G];    // q8_0: -1152 * sum of the lane's 16 q values (K byte bias)
   float vw[G];       // q8_0: sum of the fp16 P.V weights (V byte bias 1152 removed at the end)
+  // q8_0 scores on MFMA: q of head 4*g + lane%4 over the lane's 16 dims as
+  // 16-bit fixed point Q = 256 * hi + lo (q ~ Q * sq), hi and lo as int8
+  // operands in four 4-dim steps; sq per head of the lane's 16 dims
+  int qi[(G + 3) / 4][2][4];
+  float sq[G];
 };
 
 template <int D, bool Q8>
@@ -280,15 +285,49 @@ struct tile_regs {
 
 // One tile: two tokens per lane group (t0, t1).  MASKED handles the split's
 // tail and invalid pages (ok0/ok1 false).
-template <int D, int G, bool Q8, bool MASKED>
+template <int D, int G, bool Q8, bool MASKED, bool MQK>
 __device__ __forceinline__ void consume_tile(decode_state<D, G, Q8> &S, const tile_regs<D, Q8> &T,
                                              bool ok0, bool ok1, float c) {
   constexpr int LPT = D / 16;
+  float y0[G], y1[G];
+  if constexpr (MQK) {
+    // q8_0 scores on v_mfma_i32_4x4x4i8: each 4-lane block holds 4 tokens
+    // (B columns, the raw K bytes) of one 16-dim chunk and the q of 4 heads
+    // (A rows); lane 4b+j receives the 4 heads' sums for its token j over
+    // the chunk, exact in int32 (hi and lo of q separately).
+    static_assert(Q8, "integer scores need q8_0 keys");
+    const uint32_t kw0[4] = {T.k0.a.x, T.k0.a.y, T.k0.a.z, T.k0.a.w};
+    const uint32_t kw1[4] = {T.k1.a.x, T.k1.a.y, T.k1.a.z, T.k1.a.w};
+    const float ks0 = f16_bits_to_f32(static_cast<uint16_t>(T.k0.d)) * c;
+    const float ks1 = f16_bits_to_f32(static_cast<uint16_t>(T.k1.d)) * c;
+#pragma unroll
+    for (int g4 = 0; g4 < (G + 3) / 4; ++g4) {
+      int4_t h0 = {0, 0, 0, 0}, l0 = h0, h1 = h0, l1 = h0;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        h0 = __builtin_amdgcn_mfma_i32_4x4x4i8(S.qi[g4][0][m], static_cast<int>(kw0[m]), h0, 0, 0, 0);
+        h1 = __builtin_amdgcn_mfma_i32_4x4x4i8(S.qi[g4][0][m], static_cast<int>(kw1[m]), h1, 0, 0, 0);
+        l0 = __builtin_amdgcn_mfma_i32_4x4x4i8(S.qi[g4][1][m], static_cast<int>(kw0[m]), l0, 0, 0, 0);
+        l1 = __builtin_amdgcn_mfma_i32_4x4x4i8(S.qi[g4][1][m], static_cast<int>(kw1[m]), l1, 0, 0, 0);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int h = 4 * g4 + r;
+        if (h < G) {
+          y0[h] = chunk_sum<LPT>(static_cast<float>(h0[r] * 256 + l0[r]) * (S.sq[h] * ks0));
+          y1[h] = chunk_sum<LPT>(static_cast<float>(h1[r] * 256 + l1[r]) * (S.sq[h] * ks1));
+          if constexpr (MASKED) {
+            y0[h] = ok0 ? y0[h] : -INFINITY;
+            y1[h] = ok1 ? y1[h] : -INFINITY;
+          }
+        }
+      }
+    }
+  } else {
   half2_t kh0[8], kh1[8];
   float ks0, ks1;
   to_half<D, Q8>(T.k0, kh0, ks0);
   to_half<D, Q8>(T.k1, kh1, ks1);
-  float y0[G], y1[G];
   if constexpr (Q8) {  // the softmax scale folds into each token's block scale
     ks0 *= c;
     ks1 *= c;
@@ -313,6 +352,7 @@ __device__ __forceinline__ void consume_tile(decode_state<D, G, Q8> &S, const ti
       y0[h] = ok0 ? y0[h] : -INFINITY;
       y1[h] = ok1 ? y1[h] : -INFINITY;
     }
+  }
   }
 
   // V operands: both pools pair the two tokens per dimension for
@@ -398,7 +438,12 @@ __device__ __forceinline__ void consume_tile(decode_state<D, G, Q8> &S, const ti
 // UNIFORM: block_tokens is a multiple of the wave's lane-group count NGW, so
 // every row of a (tile, half) lies in one page: the page id is moved to a
 // scalar register once per half-tile and each lane adds a fixed offset.
-template <int D, int G, bool Q8, bool UNIFORM, int WPB, int NB>
+//
+// MQK (q8_0, head_dim <= 256): scores on integer MFMA.  The lane layout
+// then puts the 4 tokens of an MFMA block in lane bits 0-1 and the 16-dim
+// chunk in the bits above them: lane = j + 4 * chunk + 4 * LPT * q holds
+// chunk `chunk` of token j + 4 * q of each half-tile.
+template <int D, int G, bool Q8, bool UNIFORM, int WPB, int NB, bool MQK>
 __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
   constexpr int LPT = D / 16;         // lanes per token row
   constexpr int NGW = k_wave / LPT;   // token groups per wave
@@ -426,8 +471,14 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
   const int32_t start = split * P.tokens_per_split;
   const int32_t bt = P.L.block_tokens;
   const int32_t first_page = start / bt;
-  const int32_t lane_in_row = lane % LPT;
-  const int32_t grp = lane / LPT;
+  // lane_in_row: the lane's 16-dim chunk of a row; grp: its token of a
+  // half-tile
+  const int32_t lane_in_row = MQK ? (lane >> 2) % LPT : lane % LPT;
+  const int32_t grp = MQK ? (lane & 3) + 4 * (lane / (4 * LPT)) : lane / LPT;
+  // lane distance to the other 16 dims of a q8_0 block, and to the lanes of
+  // the same dims in the token groups merged at the end (bit r of grp)
+  constexpr int block_partner = MQK ? 4 : 1;
+  auto grp_mask = [](int r) { return MQK ? (r < 2 ? 1 << r : LPT << r) : LPT << r; };
   float4_t qraw[G][4];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
@@ -490,6 +541,37 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
       qsum += static_cast<float>(S.qh[h][j].x) + static_cast<float>(S.qh[h][j].y);
     }
     S.kbias[h] = -1152.0f * qsum;
+    if constexpr (MQK) {
+      float mx = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        mx = fmaxf(mx, fmaxf(fabsf(static_cast<float>(S.qh[h][j].x)),
+                             fabsf(static_cast<float>(S.qh[h][j].y))));
+      }
+      // |Q| <= 32639 keeps hi = (Q + 128) >> 8 inside int8
+      S.sq[h] = mx / 32639.0f;
+      const float inv = mx > 0.0f ? 32639.0f / mx : 0.0f;
+      uint32_t hw[4] = {0u, 0u, 0u, 0u}, lw[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const half2_t pr = S.qh[h][i / 2];
+        const float qv = static_cast<float>(i % 2 == 0 ? pr.x : pr.y);
+        const int32_t Q = static_cast<int32_t>(__builtin_rintf(qv * inv));
+        const int32_t hi = (Q + 128) >> 8;
+        const int32_t lo = Q - hi * 256;
+        hw[i / 4] |= (static_cast<uint32_t>(hi) & 0xFFu) << (8 * (i % 4));
+        lw[i / 4] |= (static_cast<uint32_t>(lo) & 0xFFu) << (8 * (i % 4));
+      }
+      // A-operand row of this lane: head 4 * g + lane % 4 (zero past G)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        if (h % 4 == 0) S.qi[h / 4][0][m] = S.qi[h / 4][1][m] = 0;
+        if (h % 4 == (lane & 3)) {
+          S.qi[h / 4][0][m] = static_cast<int>(hw[m]);
+          S.qi[h / 4][1][m] = static_cast<int>(lw[m]);
+        }
+      }
+    }
     S.m[h] = -INFINITY;
     S.l[h] = 0.0f;
     if constexpr (Q8) S.vw[h] = 0.0f;
@@ -521,8 +603,8 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
     const uint32_t page = s_pages[p / bt - first_page];
     new_ok = page != 0xFFFFFFFFu;
     const uint64_t row = (static_cast<uint64_t>(seq) * P.L.n_head_kv + kvh) * D;
-    new_row_regs<D, Q8>(P.new_k + row, lane_in_row, TN.k0);
-    new_row_regs<D, Q8>(P.new_v + row, lane_in_row, TN.v0);
+    new_row_regs<D, Q8>(P.new_k + row, lane_in_row, block_partner, TN.k0);
+    new_row_regs<D, Q8>(P.new_v + row, lane_in_row, block_partner, TN.v0);
     TN.k1 = TN.k0;
     TN.v1 = TN.v0;
     if (new_ok && grp == 0) {
@@ -617,7 +699,7 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
       for (int j = 0; j < NB; ++j) {
         const int32_t t = base + (NB - 1) * TT;
         load_tile(t <= last_full ? t : last_full, R[(j + NB - 1) % NB], u0, u1);
-        consume_tile<D, G, Q8, false>(S, R[j], true, true, P.c);
+        consume_tile<D, G, Q8, false, MQK>(S, R[j], true, true, P.c);
         base += TT;
       }
     }
@@ -626,7 +708,7 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
 #pragma unroll
     for (int j = 0; j + 1 < NB; ++j) {
       if (j < rem) {
-        consume_tile<D, G, Q8, false>(S, R[j], true, true, P.c);
+        consume_tile<D, G, Q8, false, MQK>(S, R[j], true, true, P.c);
         base += TT;
       }
     }
@@ -635,9 +717,9 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
     tile_regs<D, Q8> T;
     bool o0, o1;
     load_tile(base, T, o0, o1);
-    consume_tile<D, G, Q8, true>(S, T, o0, o1, P.c);
+    consume_tile<D, G, Q8, true, MQK>(S, T, o0, o1, P.c);
   }
-  if (has_new) consume_tile<D, G, Q8, true>(S, TN, new_ok && grp == 0, false, P.c);
+  if (has_new) consume_tile<D, G, Q8, true, MQK>(S, TN, new_ok && grp == 0, false, P.c);
 
   if constexpr (Q8) {
     // acc holds sum w * (q + 1152): remove the bias term
@@ -662,7 +744,7 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
   for (int h = 0; h < G; ++h) {
     M[h] = S.m[h];
 #pragma unroll
-    for (int mask = LPT; mask < k_wave; mask <<= 1) M[h] = fmaxf(M[h], wave_shfl_xor(M[h], mask));
+    for (int r = 0; r < R; ++r) M[h] = fmaxf(M[h], wave_shfl_xor(M[h], grp_mask(r)));
     const float ms = M[h] == -INFINITY ? 0.0f : M[h];
     const float f = fast_exp2(S.m[h] - ms);  // 0 for a lane that saw no token
     S.l[h] *= f;
@@ -672,7 +754,7 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
 #pragma unroll
   for (int h = 0; h < G; ++h) {
 #pragma unroll
-    for (int mask = LPT; mask < k_wave; mask <<= 1) S.l[h] += wave_shfl_xor(S.l[h], mask);
+    for (int r = 0; r < R; ++r) S.l[h] += wave_shfl_xor(S.l[h], grp_mask(r));
   }
   float (&v)[NCH * 4] = reinterpret_cast<float (&)[NCH * 4]>(S.acc);
 #pragma unroll
@@ -683,14 +765,14 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
     for (int k = 0; k < n / 2; ++k) {
       const float send = upper ? v[k] : v[k + n / 2];
       const float keep = upper ? v[k + n / 2] : v[k];
-      v[k] = keep + wave_shfl_xor(send, LPT << r);
+      v[k] = keep + wave_shfl_xor(send, grp_mask(r));
     }
   }
   constexpr int HELD = (NCH >> RS) * 4;  // floats held: chunks first_chunk .. + HELD / 4
 #pragma unroll
   for (int r = RS; r < R; ++r) {  // more groups than chunks: sum what is held
 #pragma unroll
-    for (int k = 0; k < HELD; ++k) v[k] += wave_shfl_xor(v[k], LPT << r);
+    for (int k = 0; k < HELD; ++k) v[k] += wave_shfl_xor(v[k], grp_mask(r));
   }
   // the chunk index a lane holds: bit r of grp picks the upper half in round r
   int first_chunk = 0;
@@ -860,10 +942,11 @@ template <int D, int G, bool Q8, int WPB>
 void launch_decode_wpb(const decode_params &P, dim3 grid, hipStream_t st) {
   constexpr int NGW = k_wave / (D / 16);
   if (P.L.block_tokens % NGW == 0) {
-    hipLaunchKernelGGL((decode_kernel<D, G, Q8, true, WPB, k_decode_nb>), grid, dim3(WPB * k_wave), 0, st, P);
+    hipLaunchKernelGGL((decode_kernel<D, G, Q8, true, WPB, k_decode_nb, Q8 && D <= 256>), grid,
+                       dim3(WPB * k_wave), 0, st, P);
   } else {
-    hipLaunchKernelGGL((decode_kernel<D, G, Q8, false, WPB, k_decode_nb>), grid, dim3(WPB * k_wave), 0, st,
-                       P);
+    hipLaunchKernelGGL((decode_kernel<D, G, Q8, false, WPB, k_decode_nb, Q8 && D <= 256>), grid,
+                       dim3(WPB * k_wave), 0, st, P);
   }
 }
 

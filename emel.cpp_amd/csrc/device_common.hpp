@@ -13,6 +13,7 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef float float16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t uint4_t __attribute__((ext_vector_type(4)));
+typedef int32_t int4_t __attribute__((ext_vector_type(4)));
 
 constexpr int k_wave = 64;
 
@@ -67,6 +68,39 @@ __device__ __forceinline__ float group_sum(float v) {
   if constexpr (lanes >= 8) v += dpp<k_dpp_row_half_mirror>(v);
   if constexpr (lanes >= 16) v += dpp<k_dpp_row_mirror>(v);
   if constexpr (lanes >= 32) v += __shfl_xor(v, 16, 64);  // the neighbouring 16-lane row
+  return v;
+}
+
+constexpr int k_dpp_row_ror4 = 0x124;
+constexpr int k_dpp_row_ror8 = 0x128;
+
+// v + (v of the lane `bit` lanes away) for bit 16 or 32, by the gfx950
+// row-swap permutes: with both operands v, the two results are v and its
+// partner in some order, so every lane of the pair gets the same sum.
+template <int bit>
+__device__ __forceinline__ float pair_sum_rows(float v) {
+  static_assert(bit == 16 || bit == 32, "row pair");
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  if constexpr (bit == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return __builtin_bit_cast(float, static_cast<uint32_t>(r[0])) +
+           __builtin_bit_cast(float, static_cast<uint32_t>(r[1]));
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __builtin_bit_cast(float, static_cast<uint32_t>(r[0])) +
+           __builtin_bit_cast(float, static_cast<uint32_t>(r[1]));
+  }
+}
+
+// Sum over the `chunks` lanes that differ only in lane bits 2 .. 2 +
+// log2(chunks) - 1 (chunks in {4, 8, 16}); every lane receives the total.
+template <int chunks>
+__device__ __forceinline__ float chunk_sum(float v) {
+  static_assert(chunks == 4 || chunks == 8 || chunks == 16, "chunk count");
+  v += dpp<k_dpp_row_ror8>(v);  // lane bit 3 (rotation by 8 in a 16-lane row)
+  v += dpp<k_dpp_row_ror4>(v);  // bit 2: v is already symmetric in bit 3
+  if constexpr (chunks >= 8) v = pair_sum_rows<16>(v);
+  if constexpr (chunks >= 16) v = pair_sum_rows<32>(v);
   return v;
 }
 
