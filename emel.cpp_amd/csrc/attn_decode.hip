@@ -428,6 +428,118 @@ __device__ __forceinline__ void consume_tile(decode_state<D, G, Q8> &S, const ti
   }
 }
 
+// MPV tile (q8_0, G <= 4, MFMA lane layout): scores and P.V both on 4x4x4
+// MFMA blocks, each 4-lane block holding 4 tokens of one 16-dim chunk.
+//   scores  S^T (4 tokens x 4 heads) = K (4 x 16 dims, int8) . Q^T   (i8, 2 x 4 steps)
+//   output  O^T (4 dims x 4 heads)  += V^T (4 dims x 4 tokens) . P'^T  (f16, 4 dims steps)
+// so lane 4b+j ends each step with head j: its 4 tokens' scores, then its
+// 16 dims of O over the block's tokens, and the softmax runs per lane for
+// one head.  T.k{0,1} hold the lane's own token row (token j + 4q of each
+// half); T.v{0,1}.a hold dims 4j..4j+3 of the chunk for the block's 4
+// tokens, .d the lane's own token's V block scale.  P' = p * d_v of the
+// token (the lane's 16 dims lie in one scale block), as fp16, and the V
+// bytes are the exact fp16 values b + 1152 (the 1152 * sum P' term is
+// removed at the end through vw).  ok0/ok1: the lane's own token is valid.
+template <int D, int G, bool MASKED>
+__device__ __forceinline__ void consume_tile_mpv(decode_state<D, G, true> &S,
+                                                 const tile_regs<D, true> &T, bool ok0, bool ok1,
+                                                 float c) {
+  constexpr int LPT = D / 16;
+  float y[2][4];
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf) {
+    const row_regs<D, true> &K = hf == 0 ? T.k0 : T.k1;
+    const uint32_t kw[4] = {K.a.x, K.a.y, K.a.z, K.a.w};
+    int4_t hi = {0, 0, 0, 0}, lo = hi;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      hi = __builtin_amdgcn_mfma_i32_4x4x4i8(static_cast<int>(kw[m]), S.qi[0][0][m], hi, 0, 0, 0);
+      lo = __builtin_amdgcn_mfma_i32_4x4x4i8(static_cast<int>(kw[m]), S.qi[0][1][m], lo, 0, 0, 0);
+    }
+    // token i's K block scale comes from lane i of the block; q's scale is
+    // this lane's head's
+    const float dk = f16_bits_to_f32(static_cast<uint16_t>(K.d)) * c;
+    const float dk_b[4] = {quad_bcast<0>(dk), quad_bcast<1>(dk), quad_bcast<2>(dk),
+                           quad_bcast<3>(dk)};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      y[hf][i] = chunk_sum<LPT>(static_cast<float>(hi[i] * 256 + lo[i]) * (dk_b[i] * S.sq[0]));
+    }
+    if constexpr (MASKED) {
+      const float okf = (hf == 0 ? ok0 : ok1) ? 1.0f : 0.0f;
+      const float ok_b[4] = {quad_bcast<0>(okf), quad_bcast<1>(okf), quad_bcast<2>(okf),
+                             quad_bcast<3>(okf)};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) y[hf][i] = ok_b[i] != 0.0f ? y[hf][i] : -INFINITY;
+    }
+  }
+  float mx = y[0][0];
+#pragma unroll
+  for (int k = 1; k < 8; ++k) mx = fmaxf(mx, y[k / 4][k % 4]);
+  if (mx > S.m[0] + k_rescale) {
+    const float alpha = fast_exp2(S.m[0] - mx);  // 0 on the first valid token
+    S.m[0] = mx;
+    S.l[0] *= alpha;
+    S.vw[0] *= alpha;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) S.acc[0][i] *= alpha;
+  }
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf) {
+    const row_regs<D, true> &V = hf == 0 ? T.v0 : T.v1;
+    float dv = f16_bits_to_f32(static_cast<uint16_t>(V.d));
+    if constexpr (MASKED) dv = (hf == 0 ? ok0 : ok1) ? dv : 0.0f;  // a masked slot may hold NaN bits
+    const float dv_b[4] = {quad_bcast<0>(dv), quad_bcast<1>(dv), quad_bcast<2>(dv),
+                           quad_bcast<3>(dv)};
+    float p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      p[i] = fast_exp2(y[hf][i] - S.m[0]);
+      if constexpr (MASKED) p[i] = y[hf][i] == -INFINITY ? 0.0f : p[i];
+    }
+    S.l[0] += (p[0] + p[1]) + (p[2] + p[3]);
+    const half2_t w01 = pack_half2(p[0] * dv_b[0], p[1] * dv_b[1]);
+    const half2_t w23 = pack_half2(p[2] * dv_b[2], p[3] * dv_b[3]);
+    S.vw[0] = dot2(w01, as_half2(0x3C003C00u), S.vw[0]);
+    S.vw[0] = dot2(w23, as_half2(0x3C003C00u), S.vw[0]);
+    const half4_t pw = {w01.x, w01.y, w23.x, w23.y};
+    const uint32_t w0 = V.a.x ^ 0x80808080u, w1 = V.a.y ^ 0x80808080u;
+    const uint32_t w2 = V.a.z ^ 0x80808080u, w3 = V.a.w ^ 0x80808080u;
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      // bytes of dims 2*s2 and 2*s2+1 of tokens (0, 1) and (2, 3)
+      const uint32_t sel = s2 == 0 ? 0x05010400u : 0x07030602u;
+      const uint32_t x01 = __builtin_amdgcn_perm(w1, w0, sel);
+      const uint32_t x23 = __builtin_amdgcn_perm(w3, w2, sel);
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const uint32_t cs = e == 0 ? 0x04010400u : 0x04030402u;
+        const half2_t a01 = as_half2(__builtin_amdgcn_perm(0x64646464u, x01, cs));
+        const half2_t a23 = as_half2(__builtin_amdgcn_perm(0x64646464u, x23, cs));
+        const half4_t va = {a01.x, a01.y, a23.x, a23.y};
+        const int sdim = 2 * s2 + e;  // dim 4i + sdim of the chunk in output register i
+        float4_t o = {S.acc[0][4 * sdim], S.acc[0][4 * sdim + 1], S.acc[0][4 * sdim + 2],
+                      S.acc[0][4 * sdim + 3]};
+        o = __builtin_amdgcn_mfma_f32_4x4x4f16(va, pw, o, 0, 0, 0);
+        S.acc[0][4 * sdim] = o.x;
+        S.acc[0][4 * sdim + 1] = o.y;
+        S.acc[0][4 * sdim + 2] = o.z;
+        S.acc[0][4 * sdim + 3] = o.w;
+      }
+    }
+  }
+}
+
+template <int D, int G, bool Q8, bool MASKED, bool MQK, bool MPV>
+__device__ __forceinline__ void consume_any(decode_state<D, G, Q8> &S, const tile_regs<D, Q8> &T,
+                                            bool ok0, bool ok1, float c) {
+  if constexpr (MPV) {
+    consume_tile_mpv<D, G, MASKED>(S, T, ok0, ok1, c);
+  } else {
+    consume_tile<D, G, Q8, MASKED, MQK>(S, T, ok0, ok1, c);
+  }
+}
+
 // Workgroup = WPB waves = WPB KV heads of one sequence over one split of
 // its context; wave w owns KV head blockIdx.y*WPB + w and its G query heads.
 // All waves walk the same pages at the same time, so a workgroup reads
@@ -443,8 +555,11 @@ __device__ __forceinline__ void consume_tile(decode_state<D, G, Q8> &S, const ti
 // then puts the 4 tokens of an MFMA block in lane bits 0-1 and the 16-dim
 // chunk in the bits above them: lane = j + 4 * chunk + 4 * LPT * q holds
 // chunk `chunk` of token j + 4 * q of each half-tile.
-template <int D, int G, bool Q8, bool UNIFORM, int WPB, int NB, bool MQK>
+//
+// MPV (MQK with G <= 4 and UNIFORM): P.V on MFMA as well (consume_tile_mpv).
+template <int D, int G, bool Q8, bool UNIFORM, int WPB, int NB, bool MQK, bool MPV>
 __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
+  static_assert(!MPV || (MQK && UNIFORM && G <= 4), "MPV layout");
   constexpr int LPT = D / 16;         // lanes per token row
   constexpr int NGW = k_wave / LPT;   // token groups per wave
   constexpr int TT = 2 * NGW;         // tokens per wave tile
@@ -579,6 +694,13 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
     for (int i = 0; i < 16; ++i) S.acc[h][i] = 0.0f;
   }
 
+  if constexpr (MPV) {  // the lane's B-operand head: its scale
+    float sqo = S.sq[0];
+#pragma unroll
+    for (int h = 1; h < G; ++h) sqo = h == (lane & 3) ? S.sq[h] : sqo;
+    S.sq[0] = sqo;
+  }
+
   const uint8_t *k_base = P.k_pool + static_cast<uint64_t>(P.layer) * P.L.layer_bytes +
                           static_cast<uint64_t>(kvh) * P.L.region_bytes;
   const uint8_t *v_base = P.v_pool + static_cast<uint64_t>(P.layer) * P.L.layer_bytes +
@@ -589,6 +711,18 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
       static_cast<uint32_t>(grp) * (Q8 ? D : 2 * D) + static_cast<uint32_t>(lane_in_row) * 16u;
   const uint32_t lane_sc_off =
       static_cast<uint32_t>(grp) * (D / 16) + static_cast<uint32_t>(lane_in_row / 2) * 2u;
+  // MPV V words: dims 4j..4j+3 of the lane's chunk for the 4 tokens of its block
+  [[maybe_unused]] const uint32_t lane_off_v = static_cast<uint32_t>(grp & ~3) * D +
+                                               static_cast<uint32_t>(lane_in_row) * 16u +
+                                               static_cast<uint32_t>(lane & 3) * 4u;
+  auto load_v_quad = [&](const uint8_t *region, int32_t row0, row_regs<D, Q8> &r) {
+    if constexpr (MPV) {
+      const uint8_t *u = region + static_cast<uint32_t>(row0) * static_cast<uint32_t>(D) + lane_off_v;
+      r.a = uint4_t{load4_stream(u), load4_stream(u + D), load4_stream(u + 2 * D), load4_stream(u + 3 * D)};
+      const uint8_t *sc = region + static_cast<uint32_t>(bt) * D + static_cast<uint32_t>(row0) * (D / 16);
+      r.d = load2_stream(sc + lane_sc_off);
+    }
+  };
 
   // Fused append: the workgroup whose split holds position len - 1 stores
   // the new token and attends to it from registers after the memory tiles
@@ -605,8 +739,6 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
     const uint64_t row = (static_cast<uint64_t>(seq) * P.L.n_head_kv + kvh) * D;
     new_row_regs<D, Q8>(P.new_k + row, lane_in_row, block_partner, TN.k0);
     new_row_regs<D, Q8>(P.new_v + row, lane_in_row, block_partner, TN.v0);
-    TN.k1 = TN.k0;
-    TN.v1 = TN.v0;
     if (new_ok && grp == 0) {
       const uint64_t region = static_cast<uint64_t>(P.layer) * P.L.layer_bytes +
                               static_cast<uint64_t>(kvh) * P.L.region_bytes +
@@ -630,6 +762,17 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
         }
       }
     }
+    // (after the store, which writes the row layout) V in the block
+    // layout: token 0 of the quad only
+    if constexpr (MPV) {
+      const uint32_t wj[4] = {TN.v0.a.x, TN.v0.a.y, TN.v0.a.z, TN.v0.a.w};
+      uint32_t w = wj[0];
+#pragma unroll
+      for (int k = 1; k < 4; ++k) w = (lane & 3) == k ? wj[k] : w;
+      TN.v0.a = uint4_t{grp < 4 ? w : 0u, 0u, 0u, 0u};
+    }
+    TN.k1 = TN.k0;
+    TN.v1 = TN.v0;
   }
 
   // Loads the tile at `tbase` (rows past `end` and rows on invalid pages
@@ -652,8 +795,13 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
       const uint64_t rb = static_cast<uint64_t>(pb != 0xFFFFFFFFu ? pb : 0u) * page_bytes;
       load_row_uniform<D, Q8>(k_base + ra, rowa, lane_off, lane_sc_off, bt, T.k0);
       load_row_uniform<D, Q8>(k_base + rb, rowb, lane_off, lane_sc_off, bt, T.k1);
-      load_row_uniform<D, Q8>(v_base + ra, rowa, lane_off, lane_sc_off, bt, T.v0);
-      load_row_uniform<D, Q8>(v_base + rb, rowb, lane_off, lane_sc_off, bt, T.v1);
+      if constexpr (MPV) {
+        load_v_quad(v_base + ra, rowa, T.v0);
+        load_v_quad(v_base + rb, rowb, T.v1);
+      } else {
+        load_row_uniform<D, Q8>(v_base + ra, rowa, lane_off, lane_sc_off, bt, T.v0);
+        load_row_uniform<D, Q8>(v_base + rb, rowb, lane_off, lane_sc_off, bt, T.v1);
+      }
     } else {
       const int32_t t0r = tbase + grp;
       const int32_t t1r = tbase + grp + NGW;
@@ -699,7 +847,7 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
       for (int j = 0; j < NB; ++j) {
         const int32_t t = base + (NB - 1) * TT;
         load_tile(t <= last_full ? t : last_full, R[(j + NB - 1) % NB], u0, u1);
-        consume_tile<D, G, Q8, false, MQK>(S, R[j], true, true, P.c);
+        consume_any<D, G, Q8, false, MQK, MPV>(S, R[j], true, true, P.c);
         base += TT;
       }
     }
@@ -708,7 +856,7 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
 #pragma unroll
     for (int j = 0; j + 1 < NB; ++j) {
       if (j < rem) {
-        consume_tile<D, G, Q8, false, MQK>(S, R[j], true, true, P.c);
+        consume_any<D, G, Q8, false, MQK, MPV>(S, R[j], true, true, P.c);
         base += TT;
       }
     }
@@ -717,10 +865,81 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
     tile_regs<D, Q8> T;
     bool o0, o1;
     load_tile(base, T, o0, o1);
-    consume_tile<D, G, Q8, true, MQK>(S, T, o0, o1, P.c);
+    consume_any<D, G, Q8, true, MQK, MPV>(S, T, o0, o1, P.c);
   }
-  if (has_new) consume_tile<D, G, Q8, true, MQK>(S, TN, new_ok && grp == 0, false, P.c);
+  if (has_new) consume_any<D, G, Q8, true, MQK, MPV>(S, TN, new_ok && grp == 0, false, P.c);
 
+  if constexpr (MPV) {
+    // Lane (j, chunk, q) holds head j's 16 dims of its chunk over the tokens
+    // of its quad q: acc[4 s + i] is dim 4 i + s of the chunk.  Merge over
+    // the quad bits q (lane bits from 2 + log2(LPT)) as the general path
+    // merges its token groups: rescale to the common max, sum l, and halve
+    // the four 4-dim output chunks per exchange.
+    constexpr int RQ = __builtin_ctz(NGW / 4);
+    constexpr int RS = RQ < 2 ? RQ : 2;
+    const int32_t quad = lane / (4 * LPT);
+    const int32_t head = lane & 3;
+    float M = S.m[0];
+#pragma unroll
+    for (int r = 0; r < RQ; ++r) M = fmaxf(M, wave_shfl_xor(M, (4 * LPT) << r));
+    const float ms = M == -INFINITY ? 0.0f : M;
+    const float f = fast_exp2(S.m[0] - ms);  // 0 for a lane that saw no token
+    float l = S.l[0] * f;
+    float v[16];  // v[4 i + s]: dim 4 i + s, i.e. output chunk i in order
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int sd = 0; sd < 4; ++sd) v[4 * i + sd] = fmaf(-1152.0f, S.vw[0], S.acc[0][4 * sd + i]) * f;
+    }
+#pragma unroll
+    for (int r = 0; r < RQ; ++r) l += wave_shfl_xor(l, (4 * LPT) << r);
+#pragma unroll
+    for (int r = 0; r < RS; ++r) {
+      const int n = 16 >> r;
+      const bool upper = (quad >> r) & 1;
+#pragma unroll
+      for (int k = 0; k < n / 2; ++k) {
+        const float send = upper ? v[k] : v[k + n / 2];
+        const float keep = upper ? v[k + n / 2] : v[k];
+        v[k] = keep + wave_shfl_xor(send, (4 * LPT) << r);
+      }
+    }
+    constexpr int HELD = 16 >> RS;
+#pragma unroll
+    for (int r = RS; r < RQ; ++r) {
+#pragma unroll
+      for (int k = 0; k < HELD; ++k) v[k] += wave_shfl_xor(v[k], (4 * LPT) << r);
+    }
+    int first_chunk = 0;
+#pragma unroll
+    for (int r = 0; r < RS; ++r) first_chunk += ((quad >> r) & 1) * (4 >> (r + 1));
+    const bool writer = (quad >> RS) == 0 && head < G;
+    const uint64_t row = static_cast<uint64_t>(seq) * P.L.n_head + kvh * G + head;
+    if (P.direct_out != nullptr) {
+      if (writer) {
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+#pragma unroll
+        for (int cc = 0; cc < HELD / 4; ++cc) {
+          *reinterpret_cast<float4_t *>(P.direct_out + row * D + 16 * lane_in_row + 4 * (first_chunk + cc)) =
+              float4_t{v[4 * cc] * inv, v[4 * cc + 1] * inv, v[4 * cc + 2] * inv, v[4 * cc + 3] * inv};
+        }
+      }
+      return;
+    }
+    const uint64_t slot = row * P.max_splits + split;
+    if (writer) {
+#pragma unroll
+      for (int cc = 0; cc < HELD / 4; ++cc) {
+        *reinterpret_cast<float4_t *>(P.part_acc + slot * D + 16 * lane_in_row + 4 * (first_chunk + cc)) =
+            float4_t{v[4 * cc], v[4 * cc + 1], v[4 * cc + 2], v[4 * cc + 3]};
+      }
+    }
+    if (writer && lane_in_row == 0) {
+      P.part_ml[slot * 2] = M;
+      P.part_ml[slot * 2 + 1] = l;
+    }
+    return;
+  }
   if constexpr (Q8) {
     // acc holds sum w * (q + 1152): remove the bias term
 #pragma unroll
@@ -942,11 +1161,12 @@ template <int D, int G, bool Q8, int WPB>
 void launch_decode_wpb(const decode_params &P, dim3 grid, hipStream_t st) {
   constexpr int NGW = k_wave / (D / 16);
   if (P.L.block_tokens % NGW == 0) {
-    hipLaunchKernelGGL((decode_kernel<D, G, Q8, true, WPB, k_decode_nb, Q8 && D <= 256>), grid,
-                       dim3(WPB * k_wave), 0, st, P);
+    hipLaunchKernelGGL((decode_kernel<D, G, Q8, true, WPB, k_decode_nb, Q8 && D <= 256,
+                                      Q8 && D <= 256 && G <= 4>),
+                       grid, dim3(WPB * k_wave), 0, st, P);
   } else {
-    hipLaunchKernelGGL((decode_kernel<D, G, Q8, false, WPB, k_decode_nb, Q8 && D <= 256>), grid,
-                       dim3(WPB * k_wave), 0, st, P);
+    hipLaunchKernelGGL((decode_kernel<D, G, Q8, false, WPB, k_decode_nb, Q8 && D <= 256, false>),
+                       grid, dim3(WPB * k_wave), 0, st, P);
   }
 }
 

@@ -92,6 +92,12 @@ __device__ __forceinline__ float pair_sum_rows(float v) {
   }
 }
 
+// Value of lane `src` of each aligned group of 4 lanes (DPP quad_perm).
+template <int src>
+__device__ __forceinline__ float quad_bcast(float v) {
+  return dpp<src | (src << 2) | (src << 4) | (src << 6)>(v);
+}
+
 // Sum over the `chunks` lanes that differ only in lane bits 2 .. 2 +
 // log2(chunks) - 1 (chunks in {4, 8, 16}); every lane receives the total.
 template <int chunks>
@@ -115,6 +121,9 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // ~7.1 TB/s versus plain loads.
 __device__ __forceinline__ uint4_t load16_stream(const void *p) {
   return __builtin_nontemporal_load(reinterpret_cast<const uint4_t *>(p));
+}
+__device__ __forceinline__ uint32_t load4_stream(const void *p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(p));
 }
 __device__ __forceinline__ uint32_t load2_stream(const void *p) {
   return __builtin_nontemporal_load(reinterpret_cast<const uint16_t *>(p));

@@ -284,6 +284,9 @@ def test_decode_config4_q8_0(device):
     (16, 8, 128, 16, [1000], emelk.KV_Q8_0),                      # G=2 q8_0
     (8, 1, 128, 32, [129, 1000, 16], emelk.KV_Q8_0),              # G=8 q8_0
     (4, 4, 128, 12, [100, 7], emelk.KV_Q8_0),                     # G=1, pages not a multiple of 8
+    (8, 2, 256, 16, [1, 40, 700], emelk.KV_Q8_0),                 # head_dim 256 q8_0, G=4
+    (8, 2, 64, 16, [5, 300, 1100], emelk.KV_Q8_0),                # head_dim 64 q8_0, G=4
+    (16, 8, 64, 8, [77, 3], emelk.KV_Q8_0),                       # G=2, pages not a multiple of 16
 ])
 def test_decode_edge_shapes(device, n_head, n_kv, D, bt, lens, kv_type):
     banner(f"decode edges H={n_head} HK={n_kv} D={D} bt={bt} lens={lens} type={kv_type}")
@@ -350,6 +353,8 @@ def test_decode_step_append_then_attend(device):
     (emelk.KV_F16, 8, 8, 128, 12, [11, 40], 0),           # block_tokens not a multiple of 8
     (emelk.KV_Q8_0, 32, 8, 128, 32, [31, 32, 4000], 0xFF),
     (emelk.KV_Q8_0, 16, 8, 128, 16, [100, 1], 0),
+    (emelk.KV_Q8_0, 8, 2, 64, 16, [17, 300], 0xFF),
+    (emelk.KV_Q8_0, 8, 2, 256, 16, [2, 129], 0xFF),
 ])
 def test_decode_append_is_append_then_decode(device, kv_type, n_head, n_kv, D, bt, lens,
                                              pool_byte):
