@@ -96,7 +96,45 @@ struct decode_params {
   // through that sequence's block-table row; null otherwise.
   const int32_t *row_q_start;
   int32_t rows;
+  // Balanced splits (1) or the host plan's fixed split size (0); the host
+  // plan's split size in tiles bounds the balanced one.
+  int32_t balanced;
+  int32_t host_tiles;
 };
+
+// Balanced split plan of a batch of n_seq <= 64 sequences, the same in every
+// wave that computes it: lane i holds sequence i's length, its split count
+// s_i and the index of its first split (exclusive prefix).  Splits are tb
+// tiles of `tile` tokens, tb = ceil(T / (cap - n_seq)) over the batch's T
+// tiles, clamped to [1, host_tiles]; then sum s_i <= T / tb + n_seq <= cap
+// (or, at tb = host_tiles, <= n_seq * ceil(max tiles / host_tiles) = cap),
+// so every split has a workgroup of the grid and a workspace slot.
+// Inclusive prefix sum over the wave by DPP: shifts of 1, 2, 4 and 8 lanes
+// inside each 16-lane row, then lane 15 of a row into the next row and lane
+// 31 into the upper half (row_bcast:15 / row_bcast:31).
+__device__ __forceinline__ int32_t wave_scan_incl(int32_t x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, true);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);  // row_bcast:15, rows 1 and 3
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);  // row_bcast:31, rows 2 and 3
+  return x;
+}
+
+__device__ __forceinline__ void balanced_splits(const int32_t *__restrict__ kv_lens, int32_t n_seq,
+                                                int32_t cap, int32_t host_tiles, int32_t tile,
+                                                int32_t lane, int32_t &len_i, int32_t &s_i,
+                                                int32_t &excl_i, int32_t &tb) {
+  len_i = lane < n_seq ? kv_lens[lane] : 0;
+  const int32_t t_i = len_i > 0 ? (len_i + tile - 1) / tile : 0;
+  const int32_t incl = wave_scan_incl(t_i);
+  const int32_t T = __builtin_amdgcn_readlane(incl, k_wave - 1);
+  tb = cap > n_seq ? (T + (cap - n_seq) - 1) / (cap - n_seq) : host_tiles;
+  tb = tb < 1 ? 1 : (tb > host_tiles ? host_tiles : tb);
+  s_i = (t_i + tb - 1) / tb;
+  excl_i = wave_scan_incl(s_i) - s_i;
+}
 
 
 // 16 int8 -> 8 half2 holding b + 1152 exactly: byte b becomes the fp16 bit
@@ -567,8 +605,6 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
 
   __shared__ uint32_t s_pages[k_max_split_pages];
 
-  const int32_t split = blockIdx.x;
-  const int32_t seq = blockIdx.z;
   const int32_t tid = threadIdx.x;
   // the wave index is uniform; readfirstlane lets the compiler keep the
   // head's base pointers in scalar registers
@@ -579,11 +615,37 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
   // entries are all requested before any of them is used (the page count
   // of a split is bounded by tokens_per_split, so the entries are read
   // before the length is known).
+  // With balanced splits the workgroup first reads every length of the
+  // batch (one more round trip) and takes split w = blockIdx.x + gridDim.x *
+  // blockIdx.z of the balanced plan.  Partial of head h: row slot_base + h *
+  // slot_stride of the workspace.
+  int32_t seq = blockIdx.z;
+  int32_t split = blockIdx.x;
+  int32_t tps = P.tokens_per_split;
+  int32_t len;
+  uint64_t slot_base;
+  uint32_t slot_stride;
+  if (P.balanced) {
+    const int32_t w = blockIdx.x + gridDim.x * blockIdx.z;
+    int32_t len_i, s_i, excl_i, tb;
+    balanced_splits(P.kv_lens, gridDim.z, gridDim.x * gridDim.z, P.host_tiles, TT, lane, len_i,
+                    s_i, excl_i, tb);
+    const uint64_t hit = __builtin_amdgcn_ballot_w64(s_i > 0 && excl_i <= w && w < excl_i + s_i);
+    if (hit == 0) return;  // uniform: more workgroups than splits
+    seq = __builtin_ctzll(hit);
+    split = w - __builtin_amdgcn_readlane(excl_i, seq);
+    len = __builtin_amdgcn_readlane(len_i, seq);
+    tps = tb * TT;
+    slot_base = static_cast<uint64_t>(w) * P.L.n_head + kvh * G;
+    slot_stride = 1u;
+  } else {
+    len = P.row_q_start != nullptr ? P.row_q_start[seq / P.rows] + (seq % P.rows) + 1
+                                   : P.kv_lens[seq];
+    slot_base = (static_cast<uint64_t>(seq) * P.L.n_head + kvh * G) * P.max_splits + split;
+    slot_stride = static_cast<uint32_t>(P.max_splits);
+  }
   const int32_t table_row = P.row_q_start != nullptr ? seq / P.rows : seq;
-  const int32_t len = P.row_q_start != nullptr
-                          ? P.row_q_start[table_row] + (seq - table_row * P.rows) + 1
-                          : P.kv_lens[seq];
-  const int32_t start = split * P.tokens_per_split;
+  const int32_t start = split * tps;
   const int32_t bt = P.L.block_tokens;
   const int32_t first_page = start / bt;
   // lane_in_row: the lane's 16-dim chunk of a row; grp: its token of a
@@ -627,7 +689,7 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
     }
     return;
   }
-  int32_t end = min(len, start + P.tokens_per_split);  // lowered to the new token's position when fused
+  int32_t end = min(len, start + tps);  // lowered to the new token's position when fused
   const int32_t n_pages = (end - 1) / bt - first_page + 1;  // <= max_pages
 
   int bad = 0;
@@ -926,7 +988,7 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
       }
       return;
     }
-    const uint64_t slot = row * P.max_splits + split;
+    const uint64_t slot = slot_base + static_cast<uint64_t>(head) * slot_stride;
     if (writer) {
 #pragma unroll
       for (int cc = 0; cc < HELD / 4; ++cc) {
@@ -1019,8 +1081,7 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
 #pragma unroll
     for (int c = 0; c < HELD / 4; ++c) {
       const int ch = first_chunk + c;
-      const uint64_t slot =
-          (static_cast<uint64_t>(seq) * P.L.n_head + kvh * G + ch / 4) * P.max_splits + split;
+      const uint64_t slot = slot_base + static_cast<uint64_t>(ch / 4) * slot_stride;
       *reinterpret_cast<float4_t *>(P.part_acc + slot * D + lane_dim<D, Q8>(lane_in_row, 4 * (ch % 4))) =
           float4_t{v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]};
     }
@@ -1028,8 +1089,7 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
   if (lane == 0) {
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-      const uint64_t slot =
-          (static_cast<uint64_t>(seq) * P.L.n_head + kvh * G + h) * P.max_splits + split;
+      const uint64_t slot = slot_base + static_cast<uint64_t>(h) * slot_stride;
       P.part_ml[slot * 2] = M[h];
       P.part_ml[slot * 2 + 1] = S.l[h];
     }
@@ -1045,20 +1105,35 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
 //
 // Merges the split partials of one (sequence, head): o = sum_s 2^{m_s-M} acc_s
 // / sum_s 2^{m_s-M} l_s (m in the log2 domain, scale folded in).
-template <int D, int CH>
+template <int D, int CH, bool BAL>
 __global__ __launch_bounds__(D) void combine_kernel(const float *__restrict__ part_acc,
                                                      const float *__restrict__ part_ml,
                                                      const int32_t *__restrict__ kv_lens,
                                                      int32_t n_head, int32_t max_splits,
                                                      int32_t tokens_per_split,
-                                                     float *__restrict__ out) {
+                                                     float *__restrict__ out, int32_t n_seq,
+                                                     int32_t host_tiles, int32_t tile) {
   const int32_t row = blockIdx.x;  // seq * n_head + head
   const int32_t seq = row / n_head;
   const int32_t d = threadIdx.x;
-  const int32_t len = kv_lens[seq];
-  const int32_t n = len > 0 ? min(max_splits, (len + tokens_per_split - 1) / tokens_per_split) : 0;
-  const float *ml = part_ml + static_cast<uint64_t>(row) * max_splits * 2;
-  const float *pa = part_acc + static_cast<uint64_t>(row) * max_splits * D + d;
+  // split s of this row is workspace row base + s * stride
+  int32_t n;
+  uint64_t base;
+  [[maybe_unused]] uint64_t stride = 1u;
+  if constexpr (BAL) {
+    int32_t len_i, s_i, excl_i, tb;
+    balanced_splits(kv_lens, n_seq, n_seq * max_splits, host_tiles, tile, d % k_wave, len_i, s_i,
+                    excl_i, tb);
+    n = __builtin_amdgcn_readlane(s_i, seq);
+    base = static_cast<uint64_t>(__builtin_amdgcn_readlane(excl_i, seq)) * n_head + row % n_head;
+    stride = static_cast<uint64_t>(n_head);
+  } else {
+    const int32_t len = kv_lens[seq];
+    n = len > 0 ? min(max_splits, (len + tokens_per_split - 1) / tokens_per_split) : 0;
+    base = static_cast<uint64_t>(row) * max_splits;
+  }
+  const float *ml = part_ml + base * 2;
+  const float *pa = part_acc + base * D + d;
   // chunks of CH splits: every load of a chunk is issued before any is
   // used (one round trip for up to CH splits), with an online max across
   // chunks.  CH is 16 when a sequence has at most 16 splits, else 64
@@ -1074,9 +1149,10 @@ __global__ __launch_bounds__(D) void combine_kernel(const float *__restrict__ pa
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
       const bool in = s0 + u < n;
-      mv[u] = in ? ml[2 * (s0 + u)] : -INFINITY;
-      lv[u] = in ? ml[2 * (s0 + u) + 1] : 0.0f;
-      av[u] = in ? pa[static_cast<uint64_t>(s0 + u) * D] : 0.0f;
+      const uint64_t k = BAL ? (s0 + u) * stride : static_cast<uint64_t>(s0 + u);
+      mv[u] = in ? ml[2 * k] : -INFINITY;
+      lv[u] = in ? ml[2 * k + 1] : 0.0f;
+      av[u] = in ? pa[k * D] : 0.0f;
     }
     float cm = mv[0];
 #pragma unroll
@@ -1209,27 +1285,28 @@ bool dispatch_decode(const pool_layout &L, const decode_params &P, dim3 grid, hi
                                     : dispatch_dim<false>(L.head_dim, group, P, grid, st);
 }
 
+template <int D, int CH>
+void launch_combine_d(dim3 grid, hipStream_t st, const decode_params &P, const int32_t *kv_lens,
+                      int32_t n_head, int32_t max_splits, int32_t tps, float *out, int32_t n_seq,
+                      int32_t tile) {
+  if (P.balanced) {
+    hipLaunchKernelGGL((combine_kernel<D, CH, true>), grid, dim3(D), 0, st, P.part_acc, P.part_ml,
+                       kv_lens, n_head, max_splits, tps, out, n_seq, P.host_tiles, tile);
+  } else {
+    hipLaunchKernelGGL((combine_kernel<D, CH, false>), grid, dim3(D), 0, st, P.part_acc, P.part_ml,
+                       kv_lens, n_head, max_splits, tps, out, n_seq, P.host_tiles, tile);
+  }
+}
+
 template <int CH>
 void launch_combine_ch(int32_t head_dim, dim3 grid, hipStream_t st, const decode_params &P,
                        const int32_t *kv_lens, int32_t n_head, int32_t max_splits, int32_t tps,
-                       float *out) {
+                       float *out, int32_t n_seq, int32_t tile) {
   switch (head_dim) {
-    case 64:
-      hipLaunchKernelGGL((combine_kernel<64, CH>), grid, dim3(64), 0, st, P.part_acc, P.part_ml,
-                         kv_lens, n_head, max_splits, tps, out);
-      break;
-    case 128:
-      hipLaunchKernelGGL((combine_kernel<128, CH>), grid, dim3(128), 0, st, P.part_acc, P.part_ml,
-                         kv_lens, n_head, max_splits, tps, out);
-      break;
-    case 256:
-      hipLaunchKernelGGL((combine_kernel<256, CH>), grid, dim3(256), 0, st, P.part_acc, P.part_ml,
-                         kv_lens, n_head, max_splits, tps, out);
-      break;
-    default:
-      hipLaunchKernelGGL((combine_kernel<512, CH>), grid, dim3(512), 0, st, P.part_acc, P.part_ml,
-                         kv_lens, n_head, max_splits, tps, out);
-      break;
+    case 64: launch_combine_d<64, CH>(grid, st, P, kv_lens, n_head, max_splits, tps, out, n_seq, tile); break;
+    case 128: launch_combine_d<128, CH>(grid, st, P, kv_lens, n_head, max_splits, tps, out, n_seq, tile); break;
+    case 256: launch_combine_d<256, CH>(grid, st, P, kv_lens, n_head, max_splits, tps, out, n_seq, tile); break;
+    default: launch_combine_d<512, CH>(grid, st, P, kv_lens, n_head, max_splits, tps, out, n_seq, tile); break;
   }
 }
 
@@ -1272,6 +1349,8 @@ emel_error_type decode_rows(const pool_layout &L, const void *k_pool, const void
   P.direct_out = out;
   P.row_q_start = q_start;
   P.rows = n_q;
+  P.balanced = 0;
+  P.host_tiles = 0;
   const dim3 grid(1, L.n_head_kv / waves_per_block(L.n_head_kv), static_cast<uint32_t>(n_rows));
   if (!dispatch_decode(L, P, grid, st)) return EMELK_ERR_INVALID_REQUEST;
   return hipGetLastError() == hipSuccess ? EMELK_ERR_NONE : EMELK_ERR_BACKEND;
@@ -1363,6 +1442,10 @@ emel_error_type decode_impl(const emelk_kv_geometry *g, const void *k_pool, cons
   P.direct_out = plan.max_splits == 1 ? out : nullptr;
   P.row_q_start = nullptr;
   P.rows = 1;
+  // balanced splits for a ragged batch: every split about the same size
+  const int32_t tile = 2 * (emelk::k_wave / (L.head_dim / 16));
+  P.balanced = plan.max_splits > 1 && n_seq > 1 && n_seq <= emelk::k_wave ? 1 : 0;
+  P.host_tiles = plan.tokens_per_split / tile;
   P.k_wr = static_cast<uint8_t *>(const_cast<void *>(k_pool));
   P.v_wr = static_cast<uint8_t *>(const_cast<void *>(v_pool));
   const uint64_t acc_floats = static_cast<uint64_t>(n_seq) * L.n_head * plan.max_splits * L.head_dim;
@@ -1375,10 +1458,10 @@ emel_error_type decode_impl(const emelk_kv_geometry *g, const void *k_pool, cons
   const dim3 cgrid(n_seq * L.n_head);
   if (plan.max_splits > 16) {
     emelk::launch_combine_ch<64>(L.head_dim, cgrid, st, P, kv_lens, L.n_head, plan.max_splits,
-                                 plan.tokens_per_split, out);
+                                 plan.tokens_per_split, out, n_seq, tile);
   } else {
     emelk::launch_combine_ch<16>(L.head_dim, cgrid, st, P, kv_lens, L.n_head, plan.max_splits,
-                                 plan.tokens_per_split, out);
+                                 plan.tokens_per_split, out, n_seq, tile);
   }
   return hipGetLastError() == hipSuccess ? EMELK_ERR_NONE : EMELK_ERR_BACKEND;
 }
