@@ -253,9 +253,14 @@ emel_error_type emelk_kv_copy_blocks(const emelk_kv_geometry *g, void *k_pool, v
  * emelk_attn_decode_workspace_size(n_seq, max_kv_len) is enough for every
  * call with at most n_seq sequences and max_kv_len at most max_kv_len (the
  * split count rises as the batch shrinks, so the exact need of one call is
- * not monotone in n_seq); emelk_attn_decode_plan reports the exact split
- * plan and workspace need of one call with these arguments.  The reference
- * has no counterpart: its CPU route needs no partials. */
+ * not monotone in n_seq); emelk_attn_decode_plan reports the host split
+ * plan (tokens_per_split, n_splits per sequence) and the exact workspace need
+ * of one call with these arguments.  For 2 to 64 sequences the device
+ * rebalances the splits over the actual lengths (never more splits than
+ * n_seq * n_splits, each at most tokens_per_split tokens), so the summation
+ * order of a sequence depends on the batch's lengths; results are
+ * deterministic for the same inputs.  The reference has no counterpart: its
+ * CPU route needs no partials. */
 emel_error_type emelk_attn_decode_workspace_size(const emelk_kv_geometry *g, int32_t n_seq,
                                                  int32_t max_kv_len, uint64_t *bytes_out);
 emel_error_type emelk_attn_decode_plan(const emelk_kv_geometry *g, int32_t n_seq,

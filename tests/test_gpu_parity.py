@@ -287,9 +287,14 @@ def test_decode_config4_q8_0(device):
     (8, 2, 256, 16, [1, 40, 700], emelk.KV_Q8_0),                 # head_dim 256 q8_0, G=4
     (8, 2, 64, 16, [5, 300, 1100], emelk.KV_Q8_0),                # head_dim 64 q8_0, G=4
     (16, 8, 64, 8, [77, 3], emelk.KV_Q8_0),                       # G=2, pages not a multiple of 16
+    # ragged batches: balanced splits (up to 64 sequences) and the fixed plan past 64
+    (8, 2, 64, 16, [1 + (37 * i) % 700 for i in range(64)], emelk.KV_F16),
+    (8, 2, 128, 32, [1 + (53 * i) % 500 for i in range(70)], emelk.KV_F16),
+    (8, 2, 128, 16, [2000] + [1 + (29 * i) % 90 for i in range(40)], emelk.KV_Q8_0),
 ])
 def test_decode_edge_shapes(device, n_head, n_kv, D, bt, lens, kv_type):
-    banner(f"decode edges H={n_head} HK={n_kv} D={D} bt={bt} lens={lens} type={kv_type}")
+    banner(f"decode edges H={n_head} HK={n_kv} D={D} bt={bt} n_seq={len(lens)} "
+           f"lens={lens[:6]} type={kv_type}")
     sc = Scenario(n_layer=1, n_head=n_head, n_kv=n_kv, head_dim=D, block_tokens=bt, lens=lens,
                   seed=sum(lens), kv_type=kv_type)
     _decode_case(sc, 0, 500 + sum(lens))
