@@ -314,6 +314,9 @@ struct decode_state {
   // operands in four 4-dim steps; sq per head of the lane's 16 dims
   int qi[(G + 3) / 4][2][4];
   float sq[G];
+  // f16 scores on MFMA: fp16 q of head lane%4 over the lane's 16 dims, in
+  // four 4-dim steps (the K row's order)
+  half4_t qm[4];
 };
 
 template <int D, bool Q8>
@@ -466,42 +469,71 @@ __device__ __forceinline__ void consume_tile(decode_state<D, G, Q8> &S, const ti
   }
 }
 
-// MPV tile (q8_0, G <= 4, MFMA lane layout): scores and P.V both on 4x4x4
-// MFMA blocks, each 4-lane block holding 4 tokens of one 16-dim chunk.
-//   scores  S^T (4 tokens x 4 heads) = K (4 x 16 dims, int8) . Q^T   (i8, 2 x 4 steps)
-//   output  O^T (4 dims x 4 heads)  += V^T (4 dims x 4 tokens) . P'^T  (f16, 4 dims steps)
+// MPV tile (G <= 4, MFMA lane layout): scores and P.V both on 4x4x4 MFMA
+// blocks, each 4-lane block holding 4 tokens of one 16-dim chunk.
+//   scores  S^T (4 tokens x 4 heads) = K (4 x 16 dims) . Q^T   (4 steps of 4 dims)
+//   output  O^T (4 dims x 4 heads)  += V^T (4 dims x 4 tokens) . P'^T
 // so lane 4b+j ends each step with head j: its 4 tokens' scores, then its
 // 16 dims of O over the block's tokens, and the softmax runs per lane for
 // one head.  T.k{0,1} hold the lane's own token row (token j + 4q of each
-// half); T.v{0,1}.a hold dims 4j..4j+3 of the chunk for the block's 4
-// tokens, .d the lane's own token's V block scale.  P' = p * d_v of the
-// token (the lane's 16 dims lie in one scale block), as fp16, and the V
-// bytes are the exact fp16 values b + 1152 (the 1152 * sum P' term is
-// removed at the end through vw).  ok0/ok1: the lane's own token is valid.
-template <int D, int G, bool MASKED>
-__device__ __forceinline__ void consume_tile_mpv(decode_state<D, G, true> &S,
-                                                 const tile_regs<D, true> &T, bool ok0, bool ok1,
+// half); T.v{0,1} hold 4 dims of the chunk (mpv_dim) for the block's 4
+// tokens.
+//   q8_0: K bytes on v_mfma_i32_4x4x4_16b_i8 against q as 16-bit fixed
+//   point (hi and lo int8, exact int32 sums), scaled by the token's K block
+//   scale (from the lane that loaded it) and the lane's q scale; V.d is the
+//   lane's own token's V block scale, P' = p * d_v of each token (the lane's
+//   16 dims lie in one scale block), and the V bytes enter as the exact fp16
+//   values b + 1152 (the 1152 * sum P' term is removed at the end through
+//   vw).
+//   f16: K halves on v_mfma_f32_4x4x4_16b_f16 against q in fp16; P' = p;
+//   V.a holds tokens 0 and 1 (two words each), V.b tokens 2 and 3.
+// ok0/ok1: the lane's own token is valid.
+template <int D, bool Q8>
+__device__ __forceinline__ int mpv_dim(int chunk, int j) {  // first of the lane's 4 dims
+  if constexpr (Q8) {
+    return 16 * chunk + 4 * j;
+  } else {  // the chunk's two runs of 8 (lane_dim): j = 0, 1 in the first
+    return (j < 2 ? 0 : D / 2) + 8 * chunk + 4 * (j & 1);
+  }
+}
+
+template <int D, int G, bool Q8, bool MASKED>
+__device__ __forceinline__ void consume_tile_mpv(decode_state<D, G, Q8> &S,
+                                                 const tile_regs<D, Q8> &T, bool ok0, bool ok1,
                                                  float c) {
   constexpr int LPT = D / 16;
   float y[2][4];
 #pragma unroll
   for (int hf = 0; hf < 2; ++hf) {
-    const row_regs<D, true> &K = hf == 0 ? T.k0 : T.k1;
-    const uint32_t kw[4] = {K.a.x, K.a.y, K.a.z, K.a.w};
-    int4_t hi = {0, 0, 0, 0}, lo = hi;
+    const row_regs<D, Q8> &K = hf == 0 ? T.k0 : T.k1;
+    if constexpr (Q8) {
+      const uint32_t kw[4] = {K.a.x, K.a.y, K.a.z, K.a.w};
+      int4_t hi = {0, 0, 0, 0}, lo = hi;
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      hi = __builtin_amdgcn_mfma_i32_4x4x4i8(static_cast<int>(kw[m]), S.qi[0][0][m], hi, 0, 0, 0);
-      lo = __builtin_amdgcn_mfma_i32_4x4x4i8(static_cast<int>(kw[m]), S.qi[0][1][m], lo, 0, 0, 0);
-    }
-    // token i's K block scale comes from lane i of the block; q's scale is
-    // this lane's head's
-    const float dk = f16_bits_to_f32(static_cast<uint16_t>(K.d)) * c;
-    const float dk_b[4] = {quad_bcast<0>(dk), quad_bcast<1>(dk), quad_bcast<2>(dk),
-                           quad_bcast<3>(dk)};
+      for (int m = 0; m < 4; ++m) {
+        hi = __builtin_amdgcn_mfma_i32_4x4x4i8(static_cast<int>(kw[m]), S.qi[0][0][m], hi, 0, 0, 0);
+        lo = __builtin_amdgcn_mfma_i32_4x4x4i8(static_cast<int>(kw[m]), S.qi[0][1][m], lo, 0, 0, 0);
+      }
+      // token i's K block scale comes from lane i of the block; q's scale is
+      // this lane's head's
+      const float dk = f16_bits_to_f32(static_cast<uint16_t>(K.d)) * c;
+      const float dk_b[4] = {quad_bcast<0>(dk), quad_bcast<1>(dk), quad_bcast<2>(dk),
+                             quad_bcast<3>(dk)};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      y[hf][i] = chunk_sum<LPT>(static_cast<float>(hi[i] * 256 + lo[i]) * (dk_b[i] * S.sq[0]));
+      for (int i = 0; i < 4; ++i) {
+        y[hf][i] = chunk_sum<LPT>(static_cast<float>(hi[i] * 256 + lo[i]) * (dk_b[i] * S.sq[0]));
+      }
+    } else {
+      const uint32_t kw[8] = {K.a.x, K.a.y, K.a.z, K.a.w, K.b.x, K.b.y, K.b.z, K.b.w};
+      float4_t sc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const half2_t k01 = as_half2(kw[2 * m]), k23 = as_half2(kw[2 * m + 1]);
+        const half4_t ka = {k01.x, k01.y, k23.x, k23.y};
+        sc = __builtin_amdgcn_mfma_f32_4x4x4f16(ka, S.qm[m], sc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) y[hf][i] = chunk_sum<LPT>(sc[i]) * c;
     }
     if constexpr (MASKED) {
       const float okf = (hf == 0 ? ok0 : ok1) ? 1.0f : 0.0f;
@@ -518,17 +550,13 @@ __device__ __forceinline__ void consume_tile_mpv(decode_state<D, G, true> &S,
     const float alpha = fast_exp2(S.m[0] - mx);  // 0 on the first valid token
     S.m[0] = mx;
     S.l[0] *= alpha;
-    S.vw[0] *= alpha;
+    if constexpr (Q8) S.vw[0] *= alpha;
 #pragma unroll
     for (int i = 0; i < 16; ++i) S.acc[0][i] *= alpha;
   }
 #pragma unroll
   for (int hf = 0; hf < 2; ++hf) {
-    const row_regs<D, true> &V = hf == 0 ? T.v0 : T.v1;
-    float dv = f16_bits_to_f32(static_cast<uint16_t>(V.d));
-    if constexpr (MASKED) dv = (hf == 0 ? ok0 : ok1) ? dv : 0.0f;  // a masked slot may hold NaN bits
-    const float dv_b[4] = {quad_bcast<0>(dv), quad_bcast<1>(dv), quad_bcast<2>(dv),
-                           quad_bcast<3>(dv)};
+    const row_regs<D, Q8> &V = hf == 0 ? T.v0 : T.v1;
     float p[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -536,34 +564,68 @@ __device__ __forceinline__ void consume_tile_mpv(decode_state<D, G, true> &S,
       if constexpr (MASKED) p[i] = y[hf][i] == -INFINITY ? 0.0f : p[i];
     }
     S.l[0] += (p[0] + p[1]) + (p[2] + p[3]);
-    const half2_t w01 = pack_half2(p[0] * dv_b[0], p[1] * dv_b[1]);
-    const half2_t w23 = pack_half2(p[2] * dv_b[2], p[3] * dv_b[3]);
-    S.vw[0] = dot2(w01, as_half2(0x3C003C00u), S.vw[0]);
-    S.vw[0] = dot2(w23, as_half2(0x3C003C00u), S.vw[0]);
-    const half4_t pw = {w01.x, w01.y, w23.x, w23.y};
-    const uint32_t w0 = V.a.x ^ 0x80808080u, w1 = V.a.y ^ 0x80808080u;
-    const uint32_t w2 = V.a.z ^ 0x80808080u, w3 = V.a.w ^ 0x80808080u;
+    half4_t va[4];  // A operand of dim s: its value for the block's tokens 0..3
+    half4_t pw;
+    if constexpr (Q8) {
+      float dv = f16_bits_to_f32(static_cast<uint16_t>(V.d));
+      if constexpr (MASKED) dv = (hf == 0 ? ok0 : ok1) ? dv : 0.0f;  // a masked slot may hold NaN bits
+      const float dv_b[4] = {quad_bcast<0>(dv), quad_bcast<1>(dv), quad_bcast<2>(dv),
+                             quad_bcast<3>(dv)};
+      const half2_t w01 = pack_half2(p[0] * dv_b[0], p[1] * dv_b[1]);
+      const half2_t w23 = pack_half2(p[2] * dv_b[2], p[3] * dv_b[3]);
+      S.vw[0] = dot2(w01, as_half2(0x3C003C00u), S.vw[0]);
+      S.vw[0] = dot2(w23, as_half2(0x3C003C00u), S.vw[0]);
+      pw = half4_t{w01.x, w01.y, w23.x, w23.y};
+      const uint32_t w0 = V.a.x ^ 0x80808080u, w1 = V.a.y ^ 0x80808080u;
+      const uint32_t w2 = V.a.z ^ 0x80808080u, w3 = V.a.w ^ 0x80808080u;
 #pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2) {
-      // bytes of dims 2*s2 and 2*s2+1 of tokens (0, 1) and (2, 3)
-      const uint32_t sel = s2 == 0 ? 0x05010400u : 0x07030602u;
-      const uint32_t x01 = __builtin_amdgcn_perm(w1, w0, sel);
-      const uint32_t x23 = __builtin_amdgcn_perm(w3, w2, sel);
+      for (int s2 = 0; s2 < 2; ++s2) {
+        // bytes of dims 2*s2 and 2*s2+1 of tokens (0, 1) and (2, 3)
+        const uint32_t sel = s2 == 0 ? 0x05010400u : 0x07030602u;
+        const uint32_t x01 = __builtin_amdgcn_perm(w1, w0, sel);
+        const uint32_t x23 = __builtin_amdgcn_perm(w3, w2, sel);
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const uint32_t cs = e == 0 ? 0x04010400u : 0x04030402u;
-        const half2_t a01 = as_half2(__builtin_amdgcn_perm(0x64646464u, x01, cs));
-        const half2_t a23 = as_half2(__builtin_amdgcn_perm(0x64646464u, x23, cs));
-        const half4_t va = {a01.x, a01.y, a23.x, a23.y};
-        const int sdim = 2 * s2 + e;  // dim 4i + sdim of the chunk in output register i
-        float4_t o = {S.acc[0][4 * sdim], S.acc[0][4 * sdim + 1], S.acc[0][4 * sdim + 2],
-                      S.acc[0][4 * sdim + 3]};
-        o = __builtin_amdgcn_mfma_f32_4x4x4f16(va, pw, o, 0, 0, 0);
-        S.acc[0][4 * sdim] = o.x;
-        S.acc[0][4 * sdim + 1] = o.y;
-        S.acc[0][4 * sdim + 2] = o.z;
-        S.acc[0][4 * sdim + 3] = o.w;
+        for (int e = 0; e < 2; ++e) {
+          const uint32_t cs = e == 0 ? 0x04010400u : 0x04030402u;
+          const half2_t a01 = as_half2(__builtin_amdgcn_perm(0x64646464u, x01, cs));
+          const half2_t a23 = as_half2(__builtin_amdgcn_perm(0x64646464u, x23, cs));
+          va[2 * s2 + e] = half4_t{a01.x, a01.y, a23.x, a23.y};
+        }
       }
+    } else {
+      const half2_t w01 = pack_half2(p[0], p[1]);
+      const half2_t w23 = pack_half2(p[2], p[3]);
+      pw = half4_t{w01.x, w01.y, w23.x, w23.y};
+      // token t's dims (0, 1) in word 2t, (2, 3) in word 2t + 1 (a: t = 0, 1; b: t = 2, 3)
+      uint32_t tw[8] = {V.a.x, V.a.y, V.a.z, V.a.w, V.b.x, V.b.y, V.b.z, V.b.w};
+      if constexpr (MASKED) {  // masked slots may hold NaN bits: p = 0 would not clear them
+        const float okf = (hf == 0 ? ok0 : ok1) ? 1.0f : 0.0f;
+        const float ok_b[4] = {quad_bcast<0>(okf), quad_bcast<1>(okf), quad_bcast<2>(okf),
+                               quad_bcast<3>(okf)};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          tw[2 * t] = ok_b[t] != 0.0f ? tw[2 * t] : 0u;
+          tw[2 * t + 1] = ok_b[t] != 0.0f ? tw[2 * t + 1] : 0u;
+        }
+      }
+#pragma unroll
+      for (int sd = 0; sd < 4; ++sd) {
+        const int wi = sd / 2;                                // word of the dim
+        const uint32_t sel = sd % 2 == 0 ? 0x05040100u : 0x07060302u;  // its half
+        const half2_t a01 = as_half2(__builtin_amdgcn_perm(tw[2 + wi], tw[wi], sel));
+        const half2_t a23 = as_half2(__builtin_amdgcn_perm(tw[6 + wi], tw[4 + wi], sel));
+        va[sd] = half4_t{a01.x, a01.y, a23.x, a23.y};
+      }
+    }
+#pragma unroll
+    for (int sd = 0; sd < 4; ++sd) {  // dim sd of the lane's 4 in output register i = lane i's
+      float4_t o = {S.acc[0][4 * sd], S.acc[0][4 * sd + 1], S.acc[0][4 * sd + 2],
+                    S.acc[0][4 * sd + 3]};
+      o = __builtin_amdgcn_mfma_f32_4x4x4f16(va[sd], pw, o, 0, 0, 0);
+      S.acc[0][4 * sd] = o.x;
+      S.acc[0][4 * sd + 1] = o.y;
+      S.acc[0][4 * sd + 2] = o.z;
+      S.acc[0][4 * sd + 3] = o.w;
     }
   }
 }
@@ -572,7 +634,7 @@ template <int D, int G, bool Q8, bool MASKED, bool MQK, bool MPV>
 __device__ __forceinline__ void consume_any(decode_state<D, G, Q8> &S, const tile_regs<D, Q8> &T,
                                             bool ok0, bool ok1, float c) {
   if constexpr (MPV) {
-    consume_tile_mpv<D, G, MASKED>(S, T, ok0, ok1, c);
+    consume_tile_mpv<D, G, Q8, MASKED>(S, T, ok0, ok1, c);
   } else {
     consume_tile<D, G, Q8, MASKED, MQK>(S, T, ok0, ok1, c);
   }
@@ -602,6 +664,7 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
   constexpr int NGW = k_wave / LPT;   // token groups per wave
   constexpr int TT = 2 * NGW;         // tokens per wave tile
   constexpr int NT = WPB * k_wave;
+  constexpr uint32_t ROWB = Q8 ? D : 2 * D;  // bytes of one K/V row in a page
 
   __shared__ uint32_t s_pages[k_max_split_pages];
 
@@ -718,7 +781,17 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
       qsum += static_cast<float>(S.qh[h][j].x) + static_cast<float>(S.qh[h][j].y);
     }
     S.kbias[h] = -1152.0f * qsum;
-    if constexpr (MQK) {
+    if constexpr (MQK && !Q8) {  // own head's q for the B operand (zero past G)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        if (h == 0) S.qm[m] = half4_t{0, 0, 0, 0};
+        if (h == (lane & 3)) {
+          S.qm[m] = half4_t{S.qh[h][2 * m].x, S.qh[h][2 * m].y, S.qh[h][2 * m + 1].x,
+                            S.qh[h][2 * m + 1].y};
+        }
+      }
+    }
+    if constexpr (MQK && Q8) {
       float mx = 0.0f;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -756,7 +829,7 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
     for (int i = 0; i < 16; ++i) S.acc[h][i] = 0.0f;
   }
 
-  if constexpr (MPV) {  // the lane's B-operand head: its scale
+  if constexpr (MPV && Q8) {  // the lane's B-operand head: its scale
     float sqo = S.sq[0];
 #pragma unroll
     for (int h = 1; h < G; ++h) sqo = h == (lane & 3) ? S.sq[h] : sqo;
@@ -773,16 +846,24 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
       static_cast<uint32_t>(grp) * (Q8 ? D : 2 * D) + static_cast<uint32_t>(lane_in_row) * 16u;
   const uint32_t lane_sc_off =
       static_cast<uint32_t>(grp) * (D / 16) + static_cast<uint32_t>(lane_in_row / 2) * 2u;
-  // MPV V words: dims 4j..4j+3 of the lane's chunk for the 4 tokens of its block
-  [[maybe_unused]] const uint32_t lane_off_v = static_cast<uint32_t>(grp & ~3) * D +
-                                               static_cast<uint32_t>(lane_in_row) * 16u +
-                                               static_cast<uint32_t>(lane & 3) * 4u;
+  // MPV V words: the lane's 4 dims (mpv_dim) for the 4 tokens of its block
+  [[maybe_unused]] const uint32_t lane_off_v =
+      static_cast<uint32_t>(grp & ~3) * ROWB +
+      static_cast<uint32_t>(mpv_dim<D, Q8>(lane_in_row, lane & 3)) * (Q8 ? 1u : 2u);
   auto load_v_quad = [&](const uint8_t *region, int32_t row0, row_regs<D, Q8> &r) {
     if constexpr (MPV) {
-      const uint8_t *u = region + static_cast<uint32_t>(row0) * static_cast<uint32_t>(D) + lane_off_v;
-      r.a = uint4_t{load4_stream(u), load4_stream(u + D), load4_stream(u + 2 * D), load4_stream(u + 3 * D)};
-      const uint8_t *sc = region + static_cast<uint32_t>(bt) * D + static_cast<uint32_t>(row0) * (D / 16);
-      r.d = load2_stream(sc + lane_sc_off);
+      const uint8_t *u = region + static_cast<uint32_t>(row0) * ROWB + lane_off_v;
+      if constexpr (Q8) {
+        r.a = uint4_t{load4_stream(u), load4_stream(u + D), load4_stream(u + 2 * D),
+                      load4_stream(u + 3 * D)};
+        const uint8_t *sc = region + static_cast<uint32_t>(bt) * D + static_cast<uint32_t>(row0) * (D / 16);
+        r.d = load2_stream(sc + lane_sc_off);
+      } else {
+        const uint2_t t0 = load8_stream(u), t1 = load8_stream(u + ROWB);
+        const uint2_t t2 = load8_stream(u + 2 * ROWB), t3 = load8_stream(u + 3 * ROWB);
+        r.a = uint4_t{t0.x, t0.y, t1.x, t1.y};
+        r.b = uint4_t{t2.x, t2.y, t3.x, t3.y};
+      }
     }
   };
 
@@ -826,12 +907,23 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
     }
     // (after the store, which writes the row layout) V in the block
     // layout: token 0 of the quad only
-    if constexpr (MPV) {
+    if constexpr (MPV && Q8) {
       const uint32_t wj[4] = {TN.v0.a.x, TN.v0.a.y, TN.v0.a.z, TN.v0.a.w};
       uint32_t w = wj[0];
 #pragma unroll
       for (int k = 1; k < 4; ++k) w = (lane & 3) == k ? wj[k] : w;
       TN.v0.a = uint4_t{grp < 4 ? w : 0u, 0u, 0u, 0u};
+    } else if constexpr (MPV) {  // f16: the two words of the lane's 4 dims
+      const uint32_t wj[8] = {TN.v0.a.x, TN.v0.a.y, TN.v0.a.z, TN.v0.a.w,
+                              TN.v0.b.x, TN.v0.b.y, TN.v0.b.z, TN.v0.b.w};
+      uint32_t w0 = wj[0], w1 = wj[1];
+#pragma unroll
+      for (int k = 1; k < 4; ++k) {
+        w0 = (lane & 3) == k ? wj[2 * k] : w0;
+        w1 = (lane & 3) == k ? wj[2 * k + 1] : w1;
+      }
+      TN.v0.a = uint4_t{grp < 4 ? w0 : 0u, grp < 4 ? w1 : 0u, 0u, 0u};
+      TN.v0.b = uint4_t{0u, 0u, 0u, 0u};
     }
     TN.k1 = TN.k0;
     TN.v1 = TN.v0;
@@ -951,7 +1043,10 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
-      for (int sd = 0; sd < 4; ++sd) v[4 * i + sd] = fmaf(-1152.0f, S.vw[0], S.acc[0][4 * sd + i]) * f;
+      for (int sd = 0; sd < 4; ++sd) {
+        const float a = Q8 ? fmaf(-1152.0f, S.vw[0], S.acc[0][4 * sd + i]) : S.acc[0][4 * sd + i];
+        v[4 * i + sd] = a * f;
+      }
     }
 #pragma unroll
     for (int r = 0; r < RQ; ++r) l += wave_shfl_xor(l, (4 * LPT) << r);
@@ -982,7 +1077,8 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
 #pragma unroll
         for (int cc = 0; cc < HELD / 4; ++cc) {
-          *reinterpret_cast<float4_t *>(P.direct_out + row * D + 16 * lane_in_row + 4 * (first_chunk + cc)) =
+          *reinterpret_cast<float4_t *>(P.direct_out + row * D +
+                                        mpv_dim<D, Q8>(lane_in_row, first_chunk + cc)) =
               float4_t{v[4 * cc] * inv, v[4 * cc + 1] * inv, v[4 * cc + 2] * inv, v[4 * cc + 3] * inv};
         }
       }
@@ -992,7 +1088,8 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
     if (writer) {
 #pragma unroll
       for (int cc = 0; cc < HELD / 4; ++cc) {
-        *reinterpret_cast<float4_t *>(P.part_acc + slot * D + 16 * lane_in_row + 4 * (first_chunk + cc)) =
+        *reinterpret_cast<float4_t *>(P.part_acc + slot * D +
+                                      mpv_dim<D, Q8>(lane_in_row, first_chunk + cc)) =
             float4_t{v[4 * cc], v[4 * cc + 1], v[4 * cc + 2], v[4 * cc + 3]};
       }
     }
@@ -1237,8 +1334,10 @@ template <int D, int G, bool Q8, int WPB>
 void launch_decode_wpb(const decode_params &P, dim3 grid, hipStream_t st) {
   constexpr int NGW = k_wave / (D / 16);
   if (P.L.block_tokens % NGW == 0) {
-    hipLaunchKernelGGL((decode_kernel<D, G, Q8, true, WPB, k_decode_nb, Q8 && D <= 256,
-                                      Q8 && D <= 256 && G <= 4>),
+    // MFMA scores and P.V (MPV) up to head_dim 256 and 4 query heads per KV
+    // head; q8_0 keeps MFMA scores (MQK) past 4
+    hipLaunchKernelGGL((decode_kernel<D, G, Q8, true, WPB, k_decode_nb, D <= 256 && (Q8 || G <= 4),
+                                      D <= 256 && G <= 4>),
                        grid, dim3(WPB * k_wave), 0, st, P);
   } else {
     hipLaunchKernelGGL((decode_kernel<D, G, Q8, false, WPB, k_decode_nb, Q8 && D <= 256, false>),

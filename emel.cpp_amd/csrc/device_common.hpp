@@ -14,6 +14,7 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef float float16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t uint4_t __attribute__((ext_vector_type(4)));
 typedef int32_t int4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t uint2_t __attribute__((ext_vector_type(2)));
 
 constexpr int k_wave = 64;
 
@@ -121,6 +122,9 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // ~7.1 TB/s versus plain loads.
 __device__ __forceinline__ uint4_t load16_stream(const void *p) {
   return __builtin_nontemporal_load(reinterpret_cast<const uint4_t *>(p));
+}
+__device__ __forceinline__ uint2_t load8_stream(const void *p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const uint2_t *>(p));
 }
 __device__ __forceinline__ uint32_t load4_stream(const void *p) {
   return __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(p));
