@@ -1221,8 +1221,13 @@ __global__ __launch_bounds__(D) void combine_kernel(const float *__restrict__ pa
     int32_t len_i, s_i, excl_i, tb;
     balanced_splits(kv_lens, n_seq, n_seq * max_splits, host_tiles, tile, d % k_wave, len_i, s_i,
                     excl_i, tb);
+    // lengths past max_kv_len (outside the contract) could plan more splits
+    // than the grid ran: read only slots the grid has
+    const int32_t cap = n_seq * max_splits;
+    const int32_t first = __builtin_amdgcn_readlane(excl_i, seq);
     n = __builtin_amdgcn_readlane(s_i, seq);
-    base = static_cast<uint64_t>(__builtin_amdgcn_readlane(excl_i, seq)) * n_head + row % n_head;
+    n = first >= cap ? 0 : min(n, cap - first);
+    base = static_cast<uint64_t>(first) * n_head + row % n_head;
     stride = static_cast<uint64_t>(n_head);
   } else {
     const int32_t len = kv_lens[seq];
