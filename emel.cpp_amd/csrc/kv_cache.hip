@@ -216,17 +216,19 @@ __global__ __launch_bounds__(k_threads) void copy_blocks_kernel(pool_layout L,
   uint8_t *d = pool + L.region_offset(layer, dst, 0);
   const uint64_t n16 = L.page_bytes / 16u;
   // batches of 8 loads issued before their stores keep 8 x 16 B per thread
-  // in flight
+  // in flight; the source is read once, so its loads carry the
+  // non-temporal hint (measured 311 vs 337 us for the config-5 compaction,
+  // 218 moves x 32 layers x K,V; non-temporal stores as well: 340 us)
   constexpr int kB = 8;
   uint64_t i = threadIdx.x;
   for (; i + (kB - 1) * k_threads < n16; i += kB * k_threads) {
     uint4_t v[kB];
 #pragma unroll
-    for (int b = 0; b < kB; ++b) v[b] = load16(s + (i + b * k_threads) * 16u);
+    for (int b = 0; b < kB; ++b) v[b] = load16_stream(s + (i + b * k_threads) * 16u);
 #pragma unroll
     for (int b = 0; b < kB; ++b) store16(d + (i + b * k_threads) * 16u, v[b]);
   }
-  for (; i < n16; i += k_threads) store16(d + i * 16u, load16(s + i * 16u));
+  for (; i < n16; i += k_threads) store16(d + i * 16u, load16_stream(s + i * 16u));
 }
 
 int grid_for(uint64_t work_items) {
