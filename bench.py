@@ -849,21 +849,17 @@ def generator(args, torch, emelk, dev):
         step()
     torch.cuda.synchronize()
     eager_ms = 1e3 * (time.perf_counter() - t_start) / steps
-    # capture one step's layers, then replay them after each begin_step.
-    # Two captured copies, replayed in turn: a graph is launched again only
-    # after its previous launch has finished, so with one copy the host's
-    # begin_step for the next step could not overlap the running step.
+    # capture one step's layers, then replay them after each begin_step
     dec.begin_step(ids, 1)
-    graphs = [torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()]
-    for graph in graphs:
-        with torch.cuda.graph(graph, stream=side):
-            layers()
-    graphs[0].replay()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        layers()
+    graph.replay()
     torch.cuda.synchronize()
     t_start = time.perf_counter()
-    for i in range(steps):
+    for _ in range(steps):
         dec.begin_step(ids, 1)
-        graphs[i % 2].replay()
+        graph.replay()
     torch.cuda.synchronize()
     ms_step = 1e3 * (time.perf_counter() - t_start) / steps
     ctx_mean = CTX + args.warmup + steps + 1 + (steps + 1) / 2.0  # the graph-replayed steps
@@ -876,7 +872,7 @@ def generator(args, torch, emelk, dev):
         "data": "synthetic (seeded N(0,1) projections, seeded page permutation)",
         "config": {"workload": "llama3-8b-b64-ctx8k-generator", "n_layer": L, "batch": B,
                    "ctx": CTX, "prefill_chunk": chunk,
-                   "step_launch": "begin_step + one HIP graph of the 32 layers (two captured copies, replayed in turn)",
+                   "step_launch": "begin_step + one HIP graph of the 32 layers",
                    "parallelism": "single GPU"},
         "kv_read_GBps": round(kv_bytes / (ms_step * 1e-3) / 1e9, 1),
         "eager_ms_per_step": round(eager_ms, 4),
