@@ -96,6 +96,9 @@ def main():
                          "layer) instead of emelk_attn_decode_append")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--no-prime", action="store_true",
+                    help="start each event-timed block right after the spin kernel, "
+                         "without an untimed block first")
     ap.add_argument("--eager", action="store_true",
                     help="time the step as eager launches instead of one replayed HIP graph")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -171,16 +174,20 @@ def gpu_head_start(torch, cycles=40_000_000):
         pass
 
 
-def timed_blocks(torch, stream, launch, reps):
+def timed_blocks(torch, stream, launch, reps, prime=None):
     """HIP event time (ms) of `launch()` (a block of back-to-back calls on
     `stream`), `reps` times.  Each block is queued behind a spin kernel; a
     block whose launches were not all queued before the GPU reached its
     start event (the host stalled, e.g. freeing a large array) may hold host
-    gaps and is measured again."""
+    gaps and is measured again.  `prime()`, queued between the spin and the
+    start event, runs untimed work first, so the timed block does not start
+    on a GPU that has just idled in the spin (its clocks ramp back up)."""
     times, tries = [], 0
     while len(times) < reps and tries < 4 * reps:
         tries += 1
         gpu_head_start(torch)
+        if prime is not None:
+            prime()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
         launch()
@@ -375,7 +382,8 @@ def decode_run(args, torch, emelk, dev):
                 emelk.decode_append(g, k_pool, v_pool, layer, new_k2[layer], new_v2[layer],
                                     q[layer], out[layer], kv_lens, max_len, tables, scale, ws)
 
-    attn_avg_ms = float(np.mean(timed_blocks(torch, stream, decode_block, K))) / L
+    attn_avg_ms = float(np.mean(timed_blocks(torch, stream, decode_block, K,
+                                             prime=None if args.no_prime else decode_block))) / L
 
     # Step timing: the 32-layer step (96 launches) captured once as a HIP
     # graph and replayed K times, as a serving loop would run it.
@@ -675,7 +683,8 @@ def prefill_evict(args, torch, emelk, dev):
         for layer in range(L):
             emelk.prefill_chunk(g, k_pool, v_pool, layer, q[layer], out, qs, tables, scale)
 
-    attn_ms = float(np.mean(timed_blocks(torch, stream, chunk_block, K))) / L
+    attn_ms = float(np.mean(timed_blocks(torch, stream, chunk_block, K,
+                                         prime=None if args.no_prime else chunk_block))) / L
     # bytes the kernel must move per launch: the unique K/V of the layer
     # (prefix + chunk, every KV head), the fp32 queries and the fp32 output
     prefill_bytes = (B * HK * (P0 + NQ) * (page_bytes // (HK * BT)) * 2
