@@ -4,27 +4,33 @@
 // (text/generator/detail.hpp:3153-3230) and its contiguous flash route
 // (kernel/detail.hpp:5238-5291) with one kernel family:
 //
-//   grid  = (split, kv_head, sequence); 256 threads = 4 waves.
-//   Each workgroup streams the K and V rows of its context slice once from
-//   HBM and serves all G = n_head/n_head_kv query heads of its KV head with
-//   them (GQA sharing).  A row of D halves is split over L = D/16 lanes
-//   (32 bytes = two 16-byte loads per lane); the 256/L lane groups each own
-//   two tokens of every 2*256/L-token tile and keep an fp32 online-softmax
-//   state (m, l, acc) per head.  Scores: v_dot2_f32_f16 on fp16 q (q is
-//   rounded to fp16 as round_q_for_nonflash does, detail.hpp:2898-2903) and
-//   a DPP sum over the L lanes.  P.V: v_dot2_f32_f16 of the fp16 pair
-//   (p_t0, p_t1) against the paired V values of the two tokens (the
-//   reference also rounds probabilities to fp16, detail.hpp:3146-3149).
-//   The next tile's rows are loaded before the current tile is used.
-//   At the end the groups are merged by wave shuffles and an LDS pass, and
-//   one partial (m, l, acc[D]) per (sequence, head, split) is written.
-//   A second kernel merges the splits.
+//   grid = (split, KV-head group, sequence); a workgroup is one wave per KV
+//   head of the group (8 for 8 KV heads), all walking the same pages of one
+//   split of one sequence, so it streams whole pages.  Each wave serves the
+//   G = n_head / n_head_kv query heads of its KV head from the rows it
+//   loads (GQA sharing); the next tile's rows are loaded before the current
+//   tile is used.  q is rounded to fp16 as round_q_for_nonflash does
+//   (detail.hpp:2898-2903) and P to fp16 as the reference rounds its
+//   probabilities (detail.hpp:3146-3149); the softmax is online, in fp32,
+//   with a lazily moved reference max.
 //
-// q8_0 pools: identical structure; for scores the 16 int8 values of a lane
-// are turned into exact fp16 (biased by a constant that the dot product's
-// start value removes) with byte permutes, and the lane's block scale
-// multiplies its partial score; for P.V the int8 values of two tokens
-// become exact fp16 pairs and the token scale folds into the fp16 weight
+//   MFMA route (head_dim <= 256, G <= 4, pages holding whole wave tiles):
+//   each 4-lane block of a wave holds 4 tokens of one 16-dim chunk; scores
+//   S^T = K . Q^T and the output O^T += V^T . P^T run on 4x4x4 MFMA blocks
+//   (fp16, or for q8_0 pools integer scores with q as 16-bit fixed point),
+//   and each lane keeps one head's softmax and 16 output dims.
+//   Scalar route (other shapes): a lane holds 16 dims of two tokens, scores
+//   and P.V by v_dot2_f32_f16, a DPP sum over the row's lanes.
+//
+//   At the end each wave merges its token groups (halving exchanges) and
+//   writes one partial (m, l, acc[D]) per (sequence, head, split), or the
+//   output itself when a sequence has one split; a second kernel merges the
+//   splits.  For 2 to 64 sequences the splits are balanced over the batch's
+//   actual lengths.
+//
+// q8_0 pools keep their int8 values exact: biased fp16 (b + 1152) for the
+// fp16 operands with the bias removed through the sums of the weights, and
+// the block scales applied to the scores and folded into the fp16 weights
 // p * d_v.
 #include <hip/hip_runtime.h>
 
@@ -48,15 +54,15 @@ constexpr int k_max_split_pages = 1024;
 // spill; a read-only walk of the same 64 KiB pages tops out at 6.76 TB/s,
 // which 2 sets already reach within 5%.
 constexpr int k_decode_nb = 2;
-// q8_0 at head_dim 128 was also built with scores on MFMA
-// (v_mfma_f32_16x16x32_f16 with rows = (32-value block, head), so the int8
-// values enter exactly and each lane scales its own block): correct, 15%
-// fewer VALU instructions, but no faster (5.23 vs 5.20 TB/s) and no faster
-// with 3 or 4 tile sets in flight; the shuffles that sum the blocks and hand
-// P to the V lanes lengthen each tile's dependent chain.  Scaling K to fp16
-// before the MFMA instead breaks the 2e-3 bar on the x20-outlier data.
-// Workgroups of 4 KV heads instead of 8 ran at 4.44 vs 5.51 TB/s there, and
-// with 3 waves per SIMD (168 VGPRs, one tile set in flight) at 3.06.
+// q8_0 at head_dim 128 was first built with only the scores on MFMA
+// (v_mfma_f32_16x16x32_f16 with rows = (32-value block, head)): correct, 15%
+// fewer VALU instructions, but no faster (5.23 vs 5.20 TB/s), since the
+// shuffles that sum the blocks and hand P to the V lanes lengthened each
+// tile's dependent chain; the 4x4x4 block layout (scores and P.V both on
+// MFMA, no hand-over) is what made it faster.  Scaling K to fp16 before the
+// MFMA breaks the 2e-3 bar on the x20-outlier data.  Workgroups of 4 KV
+// heads instead of 8 ran at 4.44 vs 5.51 TB/s there, and with 3 waves per
+// SIMD (168 VGPRs, one tile set in flight) at 3.06.
 
 // Waves per workgroup = KV heads per workgroup: min(n_head_kv, 8) when it
 // divides n_head_kv, else 1.
