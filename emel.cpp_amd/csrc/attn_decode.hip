@@ -322,7 +322,7 @@ struct decode_state {
   float sq[G];
   // f16 scores on MFMA: fp16 q of head lane%4 over the lane's 16 dims, in
   // four 4-dim steps (the K row's order)
-  half4_t qm[4];
+  half4_t qm[(G + 3) / 4][4];
 };
 
 template <int D, bool Q8>
@@ -475,8 +475,9 @@ __device__ __forceinline__ void consume_tile(decode_state<D, G, Q8> &S, const ti
   }
 }
 
-// MPV tile (G <= 4, MFMA lane layout): scores and P.V both on 4x4x4 MFMA
-// blocks, each 4-lane block holding 4 tokens of one 16-dim chunk.
+// MPV tile (MFMA lane layout): scores and P.V both on 4x4x4 MFMA blocks,
+// each 4-lane block holding 4 tokens of one 16-dim chunk, one set of 4
+// query heads per pass (two sets at G = 8, lane j serving heads j, j + 4).
 //   scores  S^T (4 tokens x 4 heads) = K (4 x 16 dims) . Q^T   (4 steps of 4 dims)
 //   output  O^T (4 dims x 4 heads)  += V^T (4 dims x 4 tokens) . P'^T
 // so lane 4b+j ends each step with head j: its 4 tokens' scores, then its
@@ -508,80 +509,86 @@ __device__ __forceinline__ void consume_tile_mpv(decode_state<D, G, Q8> &S,
                                                  const tile_regs<D, Q8> &T, bool ok0, bool ok1,
                                                  float c) {
   constexpr int LPT = D / 16;
-  float y[2][4];
+  constexpr int NHS = (G + 3) / 4;  // head sets: lane j serves heads j and j + 4
+  float y[NHS][2][4];
+  [[maybe_unused]] float dk_b[2][4];
 #pragma unroll
   for (int hf = 0; hf < 2; ++hf) {
     const row_regs<D, Q8> &K = hf == 0 ? T.k0 : T.k1;
     if constexpr (Q8) {
-      const uint32_t kw[4] = {K.a.x, K.a.y, K.a.z, K.a.w};
-      int4_t hi = {0, 0, 0, 0}, lo = hi;
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        hi = __builtin_amdgcn_mfma_i32_4x4x4i8(static_cast<int>(kw[m]), S.qi[0][0][m], hi, 0, 0, 0);
-        lo = __builtin_amdgcn_mfma_i32_4x4x4i8(static_cast<int>(kw[m]), S.qi[0][1][m], lo, 0, 0, 0);
-      }
-      // token i's K block scale comes from lane i of the block; q's scale is
-      // this lane's head's
+      // token i's K block scale comes from lane i of the block
       const float dk = f16_bits_to_f32(static_cast<uint16_t>(K.d)) * c;
-      const float dk_b[4] = {quad_bcast<0>(dk), quad_bcast<1>(dk), quad_bcast<2>(dk),
-                             quad_bcast<3>(dk)};
+      dk_b[hf][0] = quad_bcast<0>(dk);
+      dk_b[hf][1] = quad_bcast<1>(dk);
+      dk_b[hf][2] = quad_bcast<2>(dk);
+      dk_b[hf][3] = quad_bcast<3>(dk);
+    }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        y[hf][i] = chunk_sum<LPT>(static_cast<float>(hi[i] * 256 + lo[i]) * (dk_b[i] * S.sq[0]));
+    for (int hs = 0; hs < NHS; ++hs) {
+      if constexpr (Q8) {
+        const uint32_t kw[4] = {K.a.x, K.a.y, K.a.z, K.a.w};
+        int4_t hi = {0, 0, 0, 0}, lo = hi;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          hi = __builtin_amdgcn_mfma_i32_4x4x4i8(static_cast<int>(kw[m]), S.qi[hs][0][m], hi, 0, 0, 0);
+          lo = __builtin_amdgcn_mfma_i32_4x4x4i8(static_cast<int>(kw[m]), S.qi[hs][1][m], lo, 0, 0, 0);
+        }
+        // q's scale is this lane's head's (S.sq[hs])
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          y[hs][hf][i] =
+              chunk_sum<LPT>(static_cast<float>(hi[i] * 256 + lo[i]) * (dk_b[hf][i] * S.sq[hs]));
+        }
+      } else {
+        const uint32_t kw[8] = {K.a.x, K.a.y, K.a.z, K.a.w, K.b.x, K.b.y, K.b.z, K.b.w};
+        float4_t sc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const half2_t k01 = as_half2(kw[2 * m]), k23 = as_half2(kw[2 * m + 1]);
+          const half4_t ka = {k01.x, k01.y, k23.x, k23.y};
+          sc = __builtin_amdgcn_mfma_f32_4x4x4f16(ka, S.qm[hs][m], sc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) y[hs][hf][i] = chunk_sum<LPT>(sc[i]) * c;
       }
-    } else {
-      const uint32_t kw[8] = {K.a.x, K.a.y, K.a.z, K.a.w, K.b.x, K.b.y, K.b.z, K.b.w};
-      float4_t sc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const half2_t k01 = as_half2(kw[2 * m]), k23 = as_half2(kw[2 * m + 1]);
-        const half4_t ka = {k01.x, k01.y, k23.x, k23.y};
-        sc = __builtin_amdgcn_mfma_f32_4x4x4f16(ka, S.qm[m], sc, 0, 0, 0);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) y[hf][i] = chunk_sum<LPT>(sc[i]) * c;
     }
     if constexpr (MASKED) {
       const float okf = (hf == 0 ? ok0 : ok1) ? 1.0f : 0.0f;
       const float ok_b[4] = {quad_bcast<0>(okf), quad_bcast<1>(okf), quad_bcast<2>(okf),
                              quad_bcast<3>(okf)};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) y[hf][i] = ok_b[i] != 0.0f ? y[hf][i] : -INFINITY;
+      for (int hs = 0; hs < NHS; ++hs) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) y[hs][hf][i] = ok_b[i] != 0.0f ? y[hs][hf][i] : -INFINITY;
+      }
     }
   }
-  float mx = y[0][0];
 #pragma unroll
-  for (int k = 1; k < 8; ++k) mx = fmaxf(mx, y[k / 4][k % 4]);
-  if (mx > S.m[0] + k_rescale) {
-    const float alpha = fast_exp2(S.m[0] - mx);  // 0 on the first valid token
-    S.m[0] = mx;
-    S.l[0] *= alpha;
-    if constexpr (Q8) S.vw[0] *= alpha;
+  for (int hs = 0; hs < NHS; ++hs) {
+    float mx = y[hs][0][0];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) S.acc[0][i] *= alpha;
+    for (int k = 1; k < 8; ++k) mx = fmaxf(mx, y[hs][k / 4][k % 4]);
+    if (mx > S.m[hs] + k_rescale) {
+      const float alpha = fast_exp2(S.m[hs] - mx);  // 0 on the first valid token
+      S.m[hs] = mx;
+      S.l[hs] *= alpha;
+      if constexpr (Q8) S.vw[hs] *= alpha;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) S.acc[hs][i] *= alpha;
+    }
   }
 #pragma unroll
   for (int hf = 0; hf < 2; ++hf) {
     const row_regs<D, Q8> &V = hf == 0 ? T.v0 : T.v1;
-    float p[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      p[i] = fast_exp2(y[hf][i] - S.m[0]);
-      if constexpr (MASKED) p[i] = y[hf][i] == -INFINITY ? 0.0f : p[i];
-    }
-    S.l[0] += (p[0] + p[1]) + (p[2] + p[3]);
     half4_t va[4];  // A operand of dim s: its value for the block's tokens 0..3
-    half4_t pw;
+    [[maybe_unused]] float dv_b[4];
     if constexpr (Q8) {
       float dv = f16_bits_to_f32(static_cast<uint16_t>(V.d));
       if constexpr (MASKED) dv = (hf == 0 ? ok0 : ok1) ? dv : 0.0f;  // a masked slot may hold NaN bits
-      const float dv_b[4] = {quad_bcast<0>(dv), quad_bcast<1>(dv), quad_bcast<2>(dv),
-                             quad_bcast<3>(dv)};
-      const half2_t w01 = pack_half2(p[0] * dv_b[0], p[1] * dv_b[1]);
-      const half2_t w23 = pack_half2(p[2] * dv_b[2], p[3] * dv_b[3]);
-      S.vw[0] = dot2(w01, as_half2(0x3C003C00u), S.vw[0]);
-      S.vw[0] = dot2(w23, as_half2(0x3C003C00u), S.vw[0]);
-      pw = half4_t{w01.x, w01.y, w23.x, w23.y};
+      dv_b[0] = quad_bcast<0>(dv);
+      dv_b[1] = quad_bcast<1>(dv);
+      dv_b[2] = quad_bcast<2>(dv);
+      dv_b[3] = quad_bcast<3>(dv);
       const uint32_t w0 = V.a.x ^ 0x80808080u, w1 = V.a.y ^ 0x80808080u;
       const uint32_t w2 = V.a.z ^ 0x80808080u, w3 = V.a.w ^ 0x80808080u;
 #pragma unroll
@@ -599,9 +606,6 @@ __device__ __forceinline__ void consume_tile_mpv(decode_state<D, G, Q8> &S,
         }
       }
     } else {
-      const half2_t w01 = pack_half2(p[0], p[1]);
-      const half2_t w23 = pack_half2(p[2], p[3]);
-      pw = half4_t{w01.x, w01.y, w23.x, w23.y};
       // token t's dims (0, 1) in word 2t, (2, 3) in word 2t + 1 (a: t = 0, 1; b: t = 2, 3)
       uint32_t tw[8] = {V.a.x, V.a.y, V.a.z, V.a.w, V.b.x, V.b.y, V.b.z, V.b.w};
       if constexpr (MASKED) {  // masked slots may hold NaN bits: p = 0 would not clear them
@@ -624,14 +628,36 @@ __device__ __forceinline__ void consume_tile_mpv(decode_state<D, G, Q8> &S,
       }
     }
 #pragma unroll
-    for (int sd = 0; sd < 4; ++sd) {  // dim sd of the lane's 4 in output register i = lane i's
-      float4_t o = {S.acc[0][4 * sd], S.acc[0][4 * sd + 1], S.acc[0][4 * sd + 2],
-                    S.acc[0][4 * sd + 3]};
-      o = __builtin_amdgcn_mfma_f32_4x4x4f16(va[sd], pw, o, 0, 0, 0);
-      S.acc[0][4 * sd] = o.x;
-      S.acc[0][4 * sd + 1] = o.y;
-      S.acc[0][4 * sd + 2] = o.z;
-      S.acc[0][4 * sd + 3] = o.w;
+    for (int hs = 0; hs < NHS; ++hs) {
+      float p[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        p[i] = fast_exp2(y[hs][hf][i] - S.m[hs]);
+        if constexpr (MASKED) p[i] = y[hs][hf][i] == -INFINITY ? 0.0f : p[i];
+      }
+      S.l[hs] += (p[0] + p[1]) + (p[2] + p[3]);
+      half4_t pw;
+      if constexpr (Q8) {
+        const half2_t w01 = pack_half2(p[0] * dv_b[0], p[1] * dv_b[1]);
+        const half2_t w23 = pack_half2(p[2] * dv_b[2], p[3] * dv_b[3]);
+        S.vw[hs] = dot2(w01, as_half2(0x3C003C00u), S.vw[hs]);
+        S.vw[hs] = dot2(w23, as_half2(0x3C003C00u), S.vw[hs]);
+        pw = half4_t{w01.x, w01.y, w23.x, w23.y};
+      } else {
+        const half2_t w01 = pack_half2(p[0], p[1]);
+        const half2_t w23 = pack_half2(p[2], p[3]);
+        pw = half4_t{w01.x, w01.y, w23.x, w23.y};
+      }
+#pragma unroll
+      for (int sd = 0; sd < 4; ++sd) {  // dim sd of the lane's 4 in output register i = lane i's
+        float4_t o = {S.acc[hs][4 * sd], S.acc[hs][4 * sd + 1], S.acc[hs][4 * sd + 2],
+                      S.acc[hs][4 * sd + 3]};
+        o = __builtin_amdgcn_mfma_f32_4x4x4f16(va[sd], pw, o, 0, 0, 0);
+        S.acc[hs][4 * sd] = o.x;
+        S.acc[hs][4 * sd + 1] = o.y;
+        S.acc[hs][4 * sd + 2] = o.z;
+        S.acc[hs][4 * sd + 3] = o.w;
+      }
     }
   }
 }
@@ -662,10 +688,11 @@ __device__ __forceinline__ void consume_any(decode_state<D, G, Q8> &S, const til
 // chunk in the bits above them: lane = j + 4 * chunk + 4 * LPT * q holds
 // chunk `chunk` of token j + 4 * q of each half-tile.
 //
-// MPV (MQK with G <= 4 and UNIFORM): P.V on MFMA as well (consume_tile_mpv).
+// MPV (MQK with UNIFORM): P.V on MFMA as well (consume_tile_mpv); a lane
+// serves one query head per set of 4 (two sets at G = 8).
 template <int D, int G, bool Q8, bool UNIFORM, int WPB, int NB, bool MQK, bool MPV>
 __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
-  static_assert(!MPV || (MQK && UNIFORM && G <= 4), "MPV layout");
+  static_assert(!MPV || (MQK && UNIFORM && G <= 8), "MPV layout");
   constexpr int LPT = D / 16;         // lanes per token row
   constexpr int NGW = k_wave / LPT;   // token groups per wave
   constexpr int TT = 2 * NGW;         // tokens per wave tile
@@ -787,13 +814,13 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
       qsum += static_cast<float>(S.qh[h][j].x) + static_cast<float>(S.qh[h][j].y);
     }
     S.kbias[h] = -1152.0f * qsum;
-    if constexpr (MQK && !Q8) {  // own head's q for the B operand (zero past G)
+    if constexpr (MQK && !Q8) {  // B operand of head set h / 4: head h % 4 == lane % 4 (zero past G)
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
-        if (h == 0) S.qm[m] = half4_t{0, 0, 0, 0};
-        if (h == (lane & 3)) {
-          S.qm[m] = half4_t{S.qh[h][2 * m].x, S.qh[h][2 * m].y, S.qh[h][2 * m + 1].x,
-                            S.qh[h][2 * m + 1].y};
+        if (h % 4 == 0) S.qm[h / 4][m] = half4_t{0, 0, 0, 0};
+        if (h % 4 == (lane & 3)) {
+          S.qm[h / 4][m] = half4_t{S.qh[h][2 * m].x, S.qh[h][2 * m].y, S.qh[h][2 * m + 1].x,
+                                   S.qh[h][2 * m + 1].y};
         }
       }
     }
@@ -835,11 +862,17 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
     for (int i = 0; i < 16; ++i) S.acc[h][i] = 0.0f;
   }
 
-  if constexpr (MPV && Q8) {  // the lane's B-operand head: its scale
-    float sqo = S.sq[0];
+  if constexpr (MPV && Q8) {  // the scales of the lane's B-operand heads, head set hs in sq[hs]
+    constexpr int NHS = (G + 3) / 4;
+    float sqo[NHS];
 #pragma unroll
-    for (int h = 1; h < G; ++h) sqo = h == (lane & 3) ? S.sq[h] : sqo;
-    S.sq[0] = sqo;
+    for (int hs = 0; hs < NHS; ++hs) {
+      sqo[hs] = 0.0f;
+#pragma unroll
+      for (int h = 4 * hs; h < 4 * hs + 4 && h < G; ++h) sqo[hs] = h % 4 == (lane & 3) ? S.sq[h] : sqo[hs];
+    }
+#pragma unroll
+    for (int hs = 0; hs < NHS; ++hs) S.sq[hs] = sqo[hs];
   }
 
   const uint8_t *k_base = P.k_pool + static_cast<uint64_t>(P.layer) * P.L.layer_bytes +
@@ -1030,78 +1063,84 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
   if (has_new) consume_any<D, G, Q8, true, MQK, MPV>(S, TN, new_ok && grp == 0, false, P.c);
 
   if constexpr (MPV) {
-    // Lane (j, chunk, q) holds head j's 16 dims of its chunk over the tokens
-    // of its quad q: acc[4 s + i] is dim 4 i + s of the chunk.  Merge over
-    // the quad bits q (lane bits from 2 + log2(LPT)) as the general path
-    // merges its token groups: rescale to the common max, sum l, and halve
-    // the four 4-dim output chunks per exchange.
+    // Lane (j, chunk, q) holds, for head set hs, head 4 hs + j's 16 dims of
+    // its chunk over the tokens of its quad q: acc[hs][4 s + i] is dim 4 i + s
+    // of the chunk.  Merge over the quad bits q (lane bits from 2 +
+    // log2(LPT)) as the general path merges its token groups: rescale to the
+    // common max, sum l, and halve the four 4-dim output chunks per exchange.
+    constexpr int NHS = (G + 3) / 4;
     constexpr int RQ = __builtin_ctz(NGW / 4);
     constexpr int RS = RQ < 2 ? RQ : 2;
-    const int32_t quad = lane / (4 * LPT);
-    const int32_t head = lane & 3;
-    float M = S.m[0];
-#pragma unroll
-    for (int r = 0; r < RQ; ++r) M = fmaxf(M, wave_shfl_xor(M, (4 * LPT) << r));
-    const float ms = M == -INFINITY ? 0.0f : M;
-    const float f = fast_exp2(S.m[0] - ms);  // 0 for a lane that saw no token
-    float l = S.l[0] * f;
-    float v[16];  // v[4 i + s]: dim 4 i + s, i.e. output chunk i in order
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int sd = 0; sd < 4; ++sd) {
-        const float a = Q8 ? fmaf(-1152.0f, S.vw[0], S.acc[0][4 * sd + i]) : S.acc[0][4 * sd + i];
-        v[4 * i + sd] = a * f;
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < RQ; ++r) l += wave_shfl_xor(l, (4 * LPT) << r);
-#pragma unroll
-    for (int r = 0; r < RS; ++r) {
-      const int n = 16 >> r;
-      const bool upper = (quad >> r) & 1;
-#pragma unroll
-      for (int k = 0; k < n / 2; ++k) {
-        const float send = upper ? v[k] : v[k + n / 2];
-        const float keep = upper ? v[k + n / 2] : v[k];
-        v[k] = keep + wave_shfl_xor(send, (4 * LPT) << r);
-      }
-    }
     constexpr int HELD = 16 >> RS;
-#pragma unroll
-    for (int r = RS; r < RQ; ++r) {
-#pragma unroll
-      for (int k = 0; k < HELD; ++k) v[k] += wave_shfl_xor(v[k], (4 * LPT) << r);
-    }
+    const int32_t quad = lane / (4 * LPT);
     int first_chunk = 0;
 #pragma unroll
     for (int r = 0; r < RS; ++r) first_chunk += ((quad >> r) & 1) * (4 >> (r + 1));
-    const bool writer = (quad >> RS) == 0 && head < G;
-    const uint64_t row = static_cast<uint64_t>(seq) * P.L.n_head + kvh * G + head;
-    if (P.direct_out != nullptr) {
-      if (writer) {
-        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
 #pragma unroll
-        for (int cc = 0; cc < HELD / 4; ++cc) {
-          *reinterpret_cast<float4_t *>(P.direct_out + row * D +
-                                        mpv_dim<D, Q8>(lane_in_row, first_chunk + cc)) =
-              float4_t{v[4 * cc] * inv, v[4 * cc + 1] * inv, v[4 * cc + 2] * inv, v[4 * cc + 3] * inv};
+    for (int hs = 0; hs < NHS; ++hs) {
+      const int32_t head = 4 * hs + (lane & 3);
+      float M = S.m[hs];
+#pragma unroll
+      for (int r = 0; r < RQ; ++r) M = fmaxf(M, wave_shfl_xor(M, (4 * LPT) << r));
+      const float ms = M == -INFINITY ? 0.0f : M;
+      const float f = fast_exp2(S.m[hs] - ms);  // 0 for a lane that saw no token
+      float l = S.l[hs] * f;
+      float v[16];  // v[4 i + s]: dim 4 i + s, i.e. output chunk i in order
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int sd = 0; sd < 4; ++sd) {
+          const float a =
+              Q8 ? fmaf(-1152.0f, S.vw[hs], S.acc[hs][4 * sd + i]) : S.acc[hs][4 * sd + i];
+          v[4 * i + sd] = a * f;
         }
       }
-      return;
-    }
-    const uint64_t slot = slot_base + static_cast<uint64_t>(head) * slot_stride;
-    if (writer) {
 #pragma unroll
-      for (int cc = 0; cc < HELD / 4; ++cc) {
-        *reinterpret_cast<float4_t *>(P.part_acc + slot * D +
-                                      mpv_dim<D, Q8>(lane_in_row, first_chunk + cc)) =
-            float4_t{v[4 * cc], v[4 * cc + 1], v[4 * cc + 2], v[4 * cc + 3]};
+      for (int r = 0; r < RQ; ++r) l += wave_shfl_xor(l, (4 * LPT) << r);
+#pragma unroll
+      for (int r = 0; r < RS; ++r) {
+        const int n = 16 >> r;
+        const bool upper = (quad >> r) & 1;
+#pragma unroll
+        for (int k = 0; k < n / 2; ++k) {
+          const float send = upper ? v[k] : v[k + n / 2];
+          const float keep = upper ? v[k + n / 2] : v[k];
+          v[k] = keep + wave_shfl_xor(send, (4 * LPT) << r);
+        }
       }
-    }
-    if (writer && lane_in_row == 0) {
-      P.part_ml[slot * 2] = M;
-      P.part_ml[slot * 2 + 1] = l;
+#pragma unroll
+      for (int r = RS; r < RQ; ++r) {
+#pragma unroll
+        for (int k = 0; k < HELD; ++k) v[k] += wave_shfl_xor(v[k], (4 * LPT) << r);
+      }
+      const bool writer = (quad >> RS) == 0 && head < G;
+      const uint64_t row = static_cast<uint64_t>(seq) * P.L.n_head + kvh * G + head;
+      if (P.direct_out != nullptr) {
+        if (writer) {
+          const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+#pragma unroll
+          for (int cc = 0; cc < HELD / 4; ++cc) {
+            *reinterpret_cast<float4_t *>(P.direct_out + row * D +
+                                          mpv_dim<D, Q8>(lane_in_row, first_chunk + cc)) =
+                float4_t{v[4 * cc] * inv, v[4 * cc + 1] * inv, v[4 * cc + 2] * inv,
+                         v[4 * cc + 3] * inv};
+          }
+        }
+        continue;
+      }
+      const uint64_t slot = slot_base + static_cast<uint64_t>(head) * slot_stride;
+      if (writer) {
+#pragma unroll
+        for (int cc = 0; cc < HELD / 4; ++cc) {
+          *reinterpret_cast<float4_t *>(P.part_acc + slot * D +
+                                        mpv_dim<D, Q8>(lane_in_row, first_chunk + cc)) =
+              float4_t{v[4 * cc], v[4 * cc + 1], v[4 * cc + 2], v[4 * cc + 3]};
+        }
+      }
+      if (writer && lane_in_row == 0) {
+        P.part_ml[slot * 2] = M;
+        P.part_ml[slot * 2 + 1] = l;
+      }
     }
     return;
   }
@@ -1345,10 +1384,8 @@ template <int D, int G, bool Q8, int WPB>
 void launch_decode_wpb(const decode_params &P, dim3 grid, hipStream_t st) {
   constexpr int NGW = k_wave / (D / 16);
   if (P.L.block_tokens % NGW == 0) {
-    // MFMA scores and P.V (MPV) up to head_dim 256 and 4 query heads per KV
-    // head; q8_0 keeps MFMA scores (MQK) past 4
-    hipLaunchKernelGGL((decode_kernel<D, G, Q8, true, WPB, k_decode_nb, D <= 256 && (Q8 || G <= 4),
-                                      D <= 256 && G <= 4>),
+    // MFMA scores and P.V (MPV) up to head_dim 256, any group size
+    hipLaunchKernelGGL((decode_kernel<D, G, Q8, true, WPB, k_decode_nb, D <= 256, D <= 256>),
                        grid, dim3(WPB * k_wave), 0, st, P);
   } else {
     hipLaunchKernelGGL((decode_kernel<D, G, Q8, false, WPB, k_decode_nb, Q8 && D <= 256, false>),
