@@ -1,5 +1,6 @@
 """Seeded sweep of decode shapes against the oracle's reference route and the
-fp64 ideal (2e-3 abs + 1e-2 rel): head_dim 64/128/256, 1-8 query heads per
+fp64 ideal (2e-3 abs + 1e-2 rel; q8_0 pools, which carry outliers, also
+allow the fp16 rounding of the probabilities): head_dim 64/128/256, 1-8 query heads per
 KV head, 1-8 KV heads, page sizes that do and do not hold a whole wave tile,
 f16 and q8_0 pools, 1-70 ragged sequences, and pools whose never-written
 bytes are NaN patterns.  It covers the decode kernel's routes together: the
@@ -10,6 +11,7 @@ import numpy as np
 import pytest
 
 import emelk
+import oracle
 from kvsetup import Scenario, assert_close
 
 pytestmark = pytest.mark.gpu
@@ -50,5 +52,22 @@ def test_decode_shape_sweep(device, case):
                   outlier_frac=0.01 if kv_type == emelk.KV_Q8_0 else 0.0)
     q = np.random.default_rng(seed + 1).standard_normal((sc.n_seq, sc.n_head * D)).astype(np.float32)
     got = sc.gpu_decode(0, q)
-    assert_close(got, sc.oracle_decode(0, q), what="gpu vs reference route")
-    assert_close(got, sc.ideal_decode(0, q), what="gpu vs fp64 ideal")
+    if kv_type == emelk.KV_F16:
+        assert_close(got, sc.oracle_decode(0, q), what="gpu vs reference route")
+        assert_close(got, sc.ideal_decode(0, q), what="gpu vs fp64 ideal")
+        return
+    # q8_0 pools carry x20 outliers.  Beyond the bar, both comparisons allow
+    # 2^-10 of sum_p p |v| per output: twice the 2^-11 bound of an fp16
+    # rounding of P, since the reference route rounds its own P too.  With
+    # outliers that sum dwarfs a cancelling output (the q8_0 prefill is held
+    # to the same allowance against the ideal).
+    scale = 1.0 / np.sqrt(D)
+    qr = oracle.fp16_to_fp32(oracle.fp32_to_fp16(q))
+    mag = np.zeros_like(got)
+    for s_, n in enumerate(sc.lens):
+        k = oracle.dequantize_q8_0(oracle.quantize_q8_0(sc.k_rows[0][s_]))
+        v = oracle.dequantize_q8_0(oracle.quantize_q8_0(sc.v_rows[0][s_]))
+        mag[s_] = oracle.attention_f64(qr[s_], k, np.abs(v), sc.n_head, n_kv, D, n, scale)
+    atol = 2e-3 + 2.0 ** -10 * mag
+    assert_close(got, sc.oracle_decode(0, q), atol=atol, what="gpu vs reference route")
+    assert_close(got, sc.ideal_decode(0, q), atol=atol, what="gpu vs fp64 ideal")
