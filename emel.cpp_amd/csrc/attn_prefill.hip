@@ -836,6 +836,11 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
   // same stretch as tile t's softmax, K staged two tiles ahead, a ring of 3
   // V buffers, 228 VGPRs): 812 vs 826 TFLOP/s, and 790 with the K reads and
   // MFMAs explicitly interleaved into the softmax (sched_group_barrier).
+  // The online softmax per 32-key sub-tile, so that sub-tile 1's score
+  // MFMAs and sub-tile 0's P.V MFMAs could issue beside the other
+  // sub-tile's softmax (240 VGPRs, no spills): 374 vs 357 us per launch
+  // at the Llama-3-8B chunk shape with the compiler's own order, and 391
+  // with sched_group_barrier interleaving (q8_0: 627 and 644 vs 621).
   // Q^T kept in LDS instead of registers (225 instead of 256 VGPRs, one
   // more LDS operand read per k-step): 801 vs 834 TFLOP/s.  Four waves of
   // 32 rows (the head_dim 256 layout) at head_dim 128: 490 vs 810.  At
