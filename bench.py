@@ -51,7 +51,7 @@ PMC_TRAFFIC_BYTES = {  # workload -> bytes; source: profiles/<kernel>_<workload>
     "llama3-8b-b64-ctx8k": 2157012657,
     "llama3-8b-q8_0-b32-ctx16k": 1150410456,
     "llama3-8b-prefill512-evict25": 287661314,
-    "llama3-8b-q8_0-prefill512-evict25": 290579074,
+    "llama3-8b-q8_0-prefill512-evict25": 290586547,
     "llama3.2-1b-b16-ctx1k-4k": 96771565,
     "qwen3-0.6b-b1-ctx512": 2615111,
     "gemma4-d256-prefill512-evict25": 105300848,

@@ -88,7 +88,13 @@ struct prefill_stage<KI, VI, true> {
 // and the remainder is a multiple of d's ulp (>= 2^-24, an fp16 subnormal
 // step) below 2^7 of them.  Two values per packed op.  Only |q * d| at or
 // beyond 65520 (outside fp16) does not hold, since hi is then infinite.
-// Returns (hi, lo).
+// Returns (hi, lo).  K is staged as both planes: the scores stay exact, since
+// a rounding of K moves a score by up to 2^-11 of sum |q k|, which the
+// softmax amplifies past the 2e-3 bar on data with x20 outliers.  V is staged
+// as hi alone: one rounding of each value (<= 2^-11 relative) enters the
+// output linearly, as the fp16 rounding of P does, at most 2^-11 of
+// sum_p p |v|; it halves the P.V MFMAs and the V^T LDS reads of q8_0 pools
+// (Llama-3-8B chunk shape: 515 vs 610 us per launch).
 __device__ __forceinline__ uint2_v q8_pair_to_f16x2(uint32_t bytes2, half2_t d2) {
   const uint32_t u = bytes2 ^ 0x8080u;
   const half2_t q = as_half2(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) -
@@ -140,11 +146,12 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
   constexpr uint32_t ROWB = Q8 ? D : 2 * D;  // bytes of one K/V row in a page
   constexpr uint32_t SROWB = D / 16;         // q8_0: bytes of one row's scales
 
-  // q8_0: a hi and a lo plane of K and of V^T (their sum is exact)
+  // q8_0: a hi and a lo plane of K (their sum is exact); V^T is one plane
+  // of fp16(q * d) for both pool types
   constexpr int PL = Q8 ? 2 : 1;
   __shared__ half_t s_k[2][PL][KT][KROW];
   constexpr int VR = 2;  // V double buffer
-  __shared__ half_t s_vt[VR][PL][D][VROW];
+  __shared__ half_t s_vt[VR][D][VROW];
   __shared__ float s_row[WAVES][32];
   __shared__ uint16_t s_ptab[k_max_seq_pages];
 
@@ -586,13 +593,13 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
         // row: chosen by the permute selector, not by selecting data
         const uint32_t sel_first = odd_first ? 0x07060302u : 0x05040100u;
         const uint32_t sel_second = odd_first ? 0x05040100u : 0x07060302u;
-        auto put = [&](uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3, int plane) {
+        auto put = [&](uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) {
           const uint2 first{__builtin_amdgcn_perm(w1, w0, sel_first),
                             __builtin_amdgcn_perm(w3, w2, sel_first)};
           const uint2 second{__builtin_amdgcn_perm(w1, w0, sel_second),
                              __builtin_amdgcn_perm(w3, w2, sel_second)};
-          *reinterpret_cast<uint2 *>(&s_vt[vbuf][plane][r0][slot]) = first;
-          *reinterpret_cast<uint2 *>(&s_vt[vbuf][plane][r0 ^ 1][slot]) = second;
+          *reinterpret_cast<uint2 *>(&s_vt[vbuf][r0][slot]) = first;
+          *reinterpret_cast<uint2 *>(&s_vt[vbuf][r0 ^ 1][slot]) = second;
         };
         if constexpr (Q8) {
           uint2_v w[4];
@@ -600,10 +607,9 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
           for (int e = 0; e < 4; ++e) {
             w[e] = q8_pair_to_f16x2(R.rv[i][e] & 0xFFFFu, as_half2((R.rv[i][e] >> 16) * 0x10001u));
           }
-          put(w[0].x, w[1].x, w[2].x, w[3].x, 0);
-          put(w[0].y, w[1].y, w[2].y, w[3].y, PL - 1);
+          put(w[0].x, w[1].x, w[2].x, w[3].x);  // the hi plane: fp16(q * d)
         } else {
-          put(R.rv[i][0], R.rv[i][1], R.rv[i][2], R.rv[i][3], 0);
+          put(R.rv[i][0], R.rv[i][1], R.rv[i][2], R.rv[i][3]);
         }
       }
     }
@@ -778,16 +784,13 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
         for (int i = 0; i < 8; ++i) pa[i] = static_cast<half_t>(s[j][8 * st + i]);
 #pragma unroll
         for (int c = 0; c < DCH; ++c) {
-#pragma unroll
-          for (int pl = 0; pl < PL; ++pl) {
-            const half8_v b = *reinterpret_cast<const half8_v *>(
-                &s_vt[buf][pl][32 * c + l32][j * k_sub + 16 * st + 8 * h]);
-            o[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, b, o[c], 0, 0, 0);
-          }
+          const half8_v b = *reinterpret_cast<const half8_v *>(
+              &s_vt[buf][32 * c + l32][j * k_sub + 16 * st + 8 * h]);
+          o[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, b, o[c], 0, 0, 0);
         }
       }
     }
-    if constexpr (!Q8) {
+    {
       // the V operand reads run four MFMAs ahead (measured 2% faster than
       // the compiler's own order at the Llama-3-8B chunk shape)
       constexpr int NPV = NS * 2 * DCH;
@@ -947,7 +950,7 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
 #pragma unroll
     for (int c = 0; c < OT16; ++c) {
       const half8_v b =
-          *reinterpret_cast<const half8_v *>(&s_vt[buf][0][16 * c + c16][8 * g16]);
+          *reinterpret_cast<const half8_v *>(&s_vt[buf][16 * c + c16][8 * g16]);
       o16[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, b, o16[c], 0, 0, 0);
     }
   };
@@ -1071,7 +1074,7 @@ extern "C" emel_error_type emelk_attn_prefill_chunk(const emelk_kv_geometry *g, 
   }
   if (L.head_dim == 512 && L.kv_type == EMELK_KV_Q8_0) {
     // q8_0 at head_dim 512: row by row through the decode kernel, as the
-    // reference's per-row loop does (the hi/lo planes do not fit the LDS).
+    // reference's per-row loop does (K's hi/lo planes do not fit the LDS).
     // f16 pools at 512 run 16 query rows per wave (M16): a wave's 32 x 512
     // O tile and Q^T operand take 384 of its 512 registers, and built that
     // way the kernel spills about 1500 registers per lane (about 350 with
@@ -1097,8 +1100,8 @@ extern "C" emel_error_type emelk_attn_prefill_chunk(const emelk_kv_geometry *g, 
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool q8 = L.kv_type == EMELK_KV_Q8_0;
-  // head_dim 256: 32-key tiles (64 spill, and q8_0's hi/lo planes of 64-key
-  // tiles would not fit the LDS)
+  // head_dim 256: 32-key tiles (64 spill, and q8_0's hi/lo K planes of
+  // 64-key tiles would not fit the LDS)
   const bool ok = L.head_dim == 512 ? emelk::launch_prefill_kt<512, 32, false, true>(P, n_seq, st)
                   : L.head_dim == 256
                       ? (q8 ? emelk::launch_prefill_kt<256, 32, true>(P, n_seq, st)

@@ -718,8 +718,9 @@ Q8_PREFILL_CASES = [
 
 @pytest.mark.parametrize("case", Q8_PREFILL_CASES, ids=[f"q8p{i}" for i in range(len(Q8_PREFILL_CASES))])
 def test_prefill_chunk_q8_0(device, case):
-    """q8_0 pools on the MFMA prefill kernel: K and V are dequantized while
-    staged (fp16(q * d), one rounding of the exact product), checked against
+    """q8_0 pools on the MFMA prefill kernel: K is dequantized while staged
+    into two fp16 planes whose sum is exactly q * d, V into fp16(q * d) (one
+    rounding of the exact product), checked against
     the oracle's q8_0 route of the reference's per-row loop and against the
     fp64 ideal over the dequantized values.  With pool_byte 0xFF every
     never-written scale is an fp16 NaN, so a slot past a sequence's end (or
