@@ -344,17 +344,35 @@ def decode_run(args, torch, emelk, dev):
 
     new_k2 = [t.view(B, HK * D) for t in new_k]
     new_v2 = [t.view(B, HK * D) for t in new_v]
+    if contiguous:
+        # the one sequence sits on pages 0.. of every region: the flash
+        # route's contiguous cache, attended without a block table
+        seq_stride = int(pages_per_seq.max()) * BT
+        assert np.array_equal(tables_h[0, :pages_per_seq[0]], np.arange(pages_per_seq[0]))
+
+    def attend(layer, store):
+        """The step's attention for one layer; store: the new token is
+        written in the same launch."""
+        if contiguous:
+            emelk.decode_contiguous(g, k_pool, v_pool, layer, q[layer], out[layer], kv_lens,
+                                    max_len, seq_stride, scale, ws,
+                                    k_rows=new_k2[layer] if store else None,
+                                    v_rows=new_v2[layer] if store else None)
+        elif store:
+            emelk.decode_append(g, k_pool, v_pool, layer, new_k2[layer], new_v2[layer],
+                                q[layer], out[layer], kv_lens, max_len, tables, scale, ws)
+        else:
+            emelk.decode(g, k_pool, v_pool, layer, q[layer], out[layer], kv_lens, max_len,
+                         tables, scale, ws)
 
     def step():
         for layer in range(L):
             if args.separate_append:
                 emelk.append(g, k_pool, v_pool, layer, new_k[layer], new_v[layer], positions,
                              tables)
-                emelk.decode(g, k_pool, v_pool, layer, q[layer], out[layer], kv_lens, max_len,
-                             tables, scale, ws)
+                attend(layer, False)
             else:  # the step's store of the new token and its attention in one launch
-                emelk.decode_append(g, k_pool, v_pool, layer, new_k2[layer], new_v2[layer],
-                                    q[layer], out[layer], kv_lens, max_len, tables, scale, ws)
+                attend(layer, True)
 
     for _ in range(args.warmup):
         step()
@@ -375,12 +393,7 @@ def decode_run(args, torch, emelk, dev):
     # calls, so the figure is the decode (+ combine) kernels' own time.
     def decode_block():
         for layer in range(L):
-            if args.separate_append:
-                emelk.decode(g, k_pool, v_pool, layer, q[layer], out[layer], kv_lens, max_len,
-                             tables, scale, ws)
-            else:
-                emelk.decode_append(g, k_pool, v_pool, layer, new_k2[layer], new_v2[layer],
-                                    q[layer], out[layer], kv_lens, max_len, tables, scale, ws)
+            attend(layer, not args.separate_append)
 
     attn_avg_ms = float(np.mean(timed_blocks(torch, stream, decode_block, K,
                                              prime=None if args.no_prime else decode_block))) / L
@@ -414,7 +427,7 @@ def decode_run(args, torch, emelk, dev):
     kv_read_layer = int(lens.sum()) * row_bytes * 2          # K and V rows attended
     q_bytes = B * H * D * 4
     o_bytes = B * H * D * 4
-    table_bytes = int(pages_per_seq.sum()) * 2
+    table_bytes = 0 if contiguous else int(pages_per_seq.sum()) * 2  # contiguous: no table
     append_bytes = B * HK * D * 4 * 2 + B * row_bytes * 2
     step_kv_bytes = kv_read_layer * L
     step_bytes = (kv_read_layer + q_bytes + o_bytes + table_bytes + append_bytes) * L
@@ -564,10 +577,12 @@ def decode_run(args, torch, emelk, dev):
                      "traffic_source": (f"profiles/decode_kernel_{args.config}.md (rocprofv3 "
                                         "--pmc FETCH_SIZE / WRITE_SIZE of an earlier run of this "
                                         "workload, copy-calibrated)") if traffic else None,
-                     "kernel": ("decode_kernel + combine_kernel (HIP events per layer call)"
-                                if args.separate_append else
-                                "decode_kernel with the fused append + combine_kernel (HIP events "
-                                "per layer call)"),
+                     "kernel": (("decode_kernel + combine_kernel (HIP events per layer call)"
+                                 if args.separate_append else
+                                 "decode_kernel with the fused append + combine_kernel (HIP events "
+                                 "per layer call)") +
+                                (", emelk_attn_decode_contiguous (no block table)"
+                                 if contiguous else "")),
                      "bytes_per_launch": kernel_bytes, "avg_launch_ms": round(attn_avg_ms, 4),
                      "decode_kernel_only": ({
                          "avg_launch_ms": dk["avg_ms"],

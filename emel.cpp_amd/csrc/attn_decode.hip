@@ -763,13 +763,19 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
   }
   constexpr int PPT = (k_max_split_pages + NT - 1) / NT;  // page entries per thread
   const int32_t max_pages = min(k_max_split_pages, P.tokens_per_split / bt + 2);
-  const uint16_t *table = P.tables + static_cast<uint64_t>(table_row) * P.table_stride;
+  // Null tables: contiguous caches, page = table_row * table_stride + block
+  // (no table read between the start and the first tile's loads).
+  const bool contiguous = P.tables == nullptr;
+  const uint64_t table_base = static_cast<uint64_t>(table_row) * P.table_stride;
+  const uint16_t *table = contiguous ? nullptr : P.tables + table_base;
   uint32_t pg[PPT];
 #pragma unroll
   for (int k = 0; k < PPT; ++k) {
     const int32_t i = tid + k * NT;
     const int32_t lb = first_page + i;
-    pg[k] = (i < max_pages && lb < P.table_stride) ? table[lb] : 0xFFFFFFFFu;
+    pg[k] = (i < max_pages && lb < P.table_stride)
+                ? (contiguous ? static_cast<uint32_t>(table_base + lb) : table[lb])
+                : 0xFFFFFFFFu;
   }
   if (start >= len) {  // uniform; the combine kernel never reads this split
     if (P.direct_out != nullptr && grp == 0) {  // nothing to attend: zero output
@@ -1564,9 +1570,9 @@ emel_error_type decode_impl(const emelk_kv_geometry *g, const void *k_pool, cons
                             const float *new_k, const float *new_v) {
   emelk::pool_layout L;
   if (emelk::make_pool_layout(g, L) != EMELK_ERR_NONE || k_pool == nullptr || v_pool == nullptr ||
-      q == nullptr || out == nullptr || kv_lens == nullptr || block_tables == nullptr ||
-      workspace == nullptr || layer < 0 || layer >= L.n_layer || n_seq <= 0 || n_seq > 65535 ||
-      max_kv_len <= 0 || table_stride <= 0 || !(scale > 0.0f) || !std::isfinite(scale)) {
+      q == nullptr || out == nullptr || kv_lens == nullptr || workspace == nullptr || layer < 0 ||
+      layer >= L.n_layer || n_seq <= 0 || n_seq > 65535 || max_kv_len <= 0 ||
+      table_stride <= 0 || !(scale > 0.0f) || !std::isfinite(scale)) {
     return EMELK_ERR_INVALID_REQUEST;
   }
   const emelk::decode_plan plan = emelk::plan_decode(L, n_seq, max_kv_len);
@@ -1621,6 +1627,7 @@ extern "C" emel_error_type emelk_attn_decode(const emelk_kv_geometry *g, const v
                                              int32_t max_kv_len, const uint16_t *block_tables,
                                              int32_t table_stride, float scale, void *workspace,
                                              uint64_t workspace_bytes, void *stream) {
+  if (block_tables == nullptr) return EMELK_ERR_INVALID_REQUEST;
   return decode_impl(g, k_pool, v_pool, layer, q, out, n_seq, kv_lens, max_kv_len, block_tables,
                      table_stride, scale, workspace, workspace_bytes, stream, nullptr, nullptr);
 }
@@ -1630,9 +1637,32 @@ extern "C" emel_error_type emelk_attn_decode_append(
     const float *v_rows, const float *q, float *out, int32_t n_seq, const int32_t *kv_lens,
     int32_t max_kv_len, const uint16_t *block_tables, int32_t table_stride, float scale,
     void *workspace, uint64_t workspace_bytes, void *stream) {
-  if (k_rows == nullptr || v_rows == nullptr) return EMELK_ERR_INVALID_REQUEST;
+  if (k_rows == nullptr || v_rows == nullptr || block_tables == nullptr) {
+    return EMELK_ERR_INVALID_REQUEST;
+  }
   return decode_impl(g, k_pool, v_pool, layer, q, out, n_seq, kv_lens, max_kv_len, block_tables,
                      table_stride, scale, workspace, workspace_bytes, stream, k_rows, v_rows);
+}
+
+// Contiguous caches (the flash route's layout, text/generator/detail.hpp:
+// 3232-3292): sequence s holds its tokens in pages s * pages_per_seq ..
+// of every (layer, KV head) region, so no block table is read.
+extern "C" emel_error_type emelk_attn_decode_contiguous(
+    const emelk_kv_geometry *g, void *k_pool, void *v_pool, int32_t layer, const float *k_rows,
+    const float *v_rows, const float *q, float *out, int32_t n_seq, const int32_t *kv_lens,
+    int32_t max_kv_len, int32_t seq_stride_tokens, float scale, void *workspace,
+    uint64_t workspace_bytes, void *stream) {
+  emelk::pool_layout L;
+  if (emelk::make_pool_layout(g, L) != EMELK_ERR_NONE || (k_rows == nullptr) != (v_rows == nullptr) ||
+      n_seq <= 0 || n_seq > 65535 || seq_stride_tokens <= 0 ||
+      seq_stride_tokens % L.block_tokens != 0 || max_kv_len > seq_stride_tokens) {
+    return EMELK_ERR_INVALID_REQUEST;
+  }
+  const int64_t pages_per_seq = seq_stride_tokens / L.block_tokens;
+  if (pages_per_seq * n_seq > L.max_blocks) return EMELK_ERR_INVALID_REQUEST;
+  return decode_impl(g, k_pool, v_pool, layer, q, out, n_seq, kv_lens, max_kv_len, nullptr,
+                     static_cast<int32_t>(pages_per_seq), scale, workspace, workspace_bytes,
+                     stream, k_rows, v_rows);
 }
 
 // ---- allocation-free variant -----------------------------------------------

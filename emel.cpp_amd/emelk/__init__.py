@@ -221,6 +221,9 @@ _SIGNATURES = [
     ("emelk_attn_decode_append", ctypes.c_uint32,
      [ctypes.POINTER(Geometry), _P, _P, ctypes.c_int32, _P, _P, _P, _P, ctypes.c_int32, _P,
       ctypes.c_int32, _P, ctypes.c_int32, ctypes.c_float, _P, ctypes.c_uint64, _P]),
+    ("emelk_attn_decode_contiguous", ctypes.c_uint32,
+     [ctypes.POINTER(Geometry), _P, _P, ctypes.c_int32, _P, _P, _P, _P, ctypes.c_int32, _P,
+      ctypes.c_int32, ctypes.c_int32, ctypes.c_float, _P, ctypes.c_uint64, _P]),
     ("emelk_attn_decode_noalloc", ctypes.c_uint32,
      [ctypes.POINTER(Geometry), _P, _P, ctypes.c_int32, _P, _P, _P, _P, ctypes.c_int32, _P,
       ctypes.c_int32, _P, ctypes.c_int32, ctypes.c_float, _P]),
@@ -610,6 +613,32 @@ def decode_append(g, k_pool, v_pool, layer, k_rows, v_rows, q, out, kv_lens, max
                                         _ptr(workspace),
                                         workspace.numel() * workspace.element_size(),
                                         _stream(stream)), "emelk_attn_decode_append")
+
+
+def decode_contiguous(g, k_pool, v_pool, layer, q, out, kv_lens, max_kv_len, seq_stride_tokens,
+                      scale, workspace, k_rows=None, v_rows=None, stream=None):
+    """Decode on contiguous caches (no block table): sequence s holds token t
+    at page s * seq_stride_tokens / block_tokens + t / block_tokens.  With
+    k_rows/v_rows the token at kv_lens - 1 is stored first."""
+    _pools(g, k_pool, v_pool)
+    if not _is_tensor(q):
+        raise TypeError("q: expected a device tensor (its first dimension is n_seq)")
+    n_seq = int(q.shape[0])
+    _rows(q, "q", n_seq, g.n_head, g.head_dim)
+    _rows(out, "out", n_seq, g.n_head, g.head_dim)
+    _need(kv_lens, "kv_lens", ("int32",), (n_seq,))
+    _need(workspace, "workspace")
+    if (k_rows is None) != (v_rows is None):
+        raise ValueError("k_rows and v_rows: both or neither")
+    if k_rows is not None:
+        _rows(k_rows, "k_rows", n_seq, 1, g.n_head_kv * g.head_dim)
+        _rows(v_rows, "v_rows", n_seq, 1, g.n_head_kv * g.head_dim)
+    _check(lib.emelk_attn_decode_contiguous(
+        ctypes.byref(g), _ptr(k_pool), _ptr(v_pool), layer,
+        _ptr(k_rows), _ptr(v_rows), _ptr(q), _ptr(out), n_seq, _ptr(kv_lens),
+        max_kv_len, seq_stride_tokens, scale, _ptr(workspace),
+        workspace.numel() * workspace.element_size(), _stream(stream)),
+        "emelk_attn_decode_contiguous")
 
 
 def prefill_chunk(g, k_pool, v_pool, layer, q, out, q_start, block_tables, scale, stream=None):

@@ -288,6 +288,28 @@ emel_error_type emelk_attn_decode_append(const emelk_kv_geometry *g, void *k_poo
                                          float scale, void *workspace, uint64_t workspace_bytes,
                                          void *stream);
 
+/* Decode on contiguous caches: the flash route's request
+ * (make_flash_attn_request, text/generator/detail.hpp:3232-3292, taken for
+ * an identity block map, generator/guards.hpp:890-906), whose K and V caches
+ * are head-major [layer][kv_head][capacity][head_dim].  Sequence s holds
+ * token t at page s * (seq_stride_tokens / block_tokens) + t / block_tokens
+ * of every (layer, KV head) region, row t % block_tokens: for one f16
+ * sequence that is exactly the flash cache layout with capacity =
+ * max_blocks * block_tokens.  No block table is read.  With k_rows and
+ * v_rows non-NULL the step's token (position kv_lens[s] - 1) is stored first,
+ * as emelk_attn_decode_append does; both NULL: attend only.  Same results as
+ * emelk_attn_decode / _append with the equivalent identity tables.
+ * seq_stride_tokens must be a multiple of block_tokens and at least
+ * max_kv_len, and n_seq * seq_stride_tokens / block_tokens at most
+ * max_blocks.  Workspace as for emelk_attn_decode. */
+emel_error_type emelk_attn_decode_contiguous(const emelk_kv_geometry *g, void *k_pool,
+                                             void *v_pool, int32_t layer, const float *k_rows,
+                                             const float *v_rows, const float *q, float *out,
+                                             int32_t n_seq, const int32_t *kv_lens,
+                                             int32_t max_kv_len, int32_t seq_stride_tokens,
+                                             float scale, void *workspace,
+                                             uint64_t workspace_bytes, void *stream);
+
 /* Allocation-free decode.  No counterpart in the reference: it is for
  * callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc).  Same results as
@@ -312,8 +334,9 @@ emel_error_type emelk_attn_decode_noalloc(const emelk_kv_geometry *g, void *k_po
  * logical positions [0, q_start[s] + r] (the chunk must already be appended).
  * Replaces the per-row store + attend loop of run_prefill
  * (text/generator/detail.hpp:4297-4372).  head_dim 64 and 128 run on MFMA,
- * f16 and q8_0 pools alike (q8_0 values enter the MFMAs exactly, as two
- * fp16 parts; values of magnitude 65520 or more do not fit), and so do
+ * f16 and q8_0 pools alike (q8_0 K values enter the score MFMAs exactly, as
+ * two fp16 parts, values of magnitude 65520 or more excepted; q8_0 V values
+ * as fp16(q * d), one rounding), and so do
  * head_dim 256 and, on f16 pools, 512.  q8_0 at head_dim 512 runs row by
  * row through the decode kernel (n_seq * n_q <= 65535, and a row's
  * context, table_stride * block_tokens tokens at most, must fit 1022

@@ -61,6 +61,23 @@ def test_kernel_entry_points_validate_before_touching_the_gpu():
     assert bad_cb.value == emelk.ERR_INVALID_REQUEST
 
 
+def test_contiguous_decode_validates_its_layout_before_touching_the_gpu():
+    g = emelk.geometry(2, 8, 2, 64, 16, 64)
+    fake = ctypes.c_void_p(256)  # never dereferenced: every call below is refused first
+    f = emelk.lib.emelk_attn_decode_contiguous
+
+    def call(n_seq=2, max_len=100, stride=128, k_rows=None, v_rows=None):
+        return f(ctypes.byref(g), fake, fake, 0, k_rows, v_rows, fake, fake, n_seq, fake,
+                 max_len, stride, 0.1, fake, 1 << 20, None)
+
+    assert call(stride=120) == emelk.ERR_INVALID_REQUEST           # not whole pages
+    assert call(max_len=129) == emelk.ERR_INVALID_REQUEST          # context past the stride
+    assert call(n_seq=9) == emelk.ERR_INVALID_REQUEST              # 9 x 8 pages > 64
+    assert call(stride=0) == emelk.ERR_INVALID_REQUEST
+    assert call(k_rows=fake) == emelk.ERR_INVALID_REQUEST          # k_rows without v_rows
+    assert call(n_seq=0) == emelk.ERR_INVALID_REQUEST
+
+
 def test_rope_table_rejects_bad_pairings_before_touching_the_gpu():
     h = ctypes.c_void_p(None)
 
