@@ -1644,9 +1644,10 @@ extern "C" emel_error_type emelk_attn_decode_append(
                      table_stride, scale, workspace, workspace_bytes, stream, k_rows, v_rows);
 }
 
-// Contiguous caches (the flash route's layout, text/generator/detail.hpp:
-// 3232-3292): sequence s holds its tokens in pages s * pages_per_seq ..
-// of every (layer, KV head) region, so no block table is read.
+// Contiguous caches: sequence s holds its tokens in pages s * pages_per_seq
+// onwards, in order, so no block table is read.  One page spanning the
+// capacity (max_blocks = 1) makes the pools the flash route's head-major
+// caches (text/generator/detail.hpp:3232-3292).
 extern "C" emel_error_type emelk_attn_decode_contiguous(
     const emelk_kv_geometry *g, void *k_pool, void *v_pool, int32_t layer, const float *k_rows,
     const float *v_rows, const float *q, float *out, int32_t n_seq, const int32_t *kv_lens,

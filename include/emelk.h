@@ -292,10 +292,11 @@ emel_error_type emelk_attn_decode_append(const emelk_kv_geometry *g, void *k_poo
  * (make_flash_attn_request, text/generator/detail.hpp:3232-3292, taken for
  * an identity block map, generator/guards.hpp:890-906), whose K and V caches
  * are head-major [layer][kv_head][capacity][head_dim].  Sequence s holds
- * token t at page s * (seq_stride_tokens / block_tokens) + t / block_tokens
- * of every (layer, KV head) region, row t % block_tokens: for one f16
- * sequence that is exactly the flash cache layout with capacity =
- * max_blocks * block_tokens.  No block table is read.  With k_rows and
+ * token t at page s * (seq_stride_tokens / block_tokens) + t / block_tokens,
+ * row t % block_tokens, of the pools' usual layout; no block table is read.
+ * With block_tokens = capacity and max_blocks = 1 (one page per layer,
+ * holding every KV head's capacity rows) the pools are exactly the flash
+ * caches, and n_seq = 1, seq_stride_tokens = capacity.  With k_rows and
  * v_rows non-NULL the step's token (position kv_lens[s] - 1) is stored first,
  * as emelk_attn_decode_append does; both NULL: attend only.  Same results as
  * emelk_attn_decode / _append with the equivalent identity tables.

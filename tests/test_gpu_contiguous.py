@@ -1,11 +1,11 @@
-"""Decode on contiguous caches (emelk_attn_decode_contiguous): the flash
-route's cache layout (make_flash_attn_request, text/generator/detail.hpp:
-3232-3292), head-major per (layer, KV head), no block table.  The kernel is
-the paged one with the page of a token computed instead of read, so every
-result must equal, bit for bit, the paged entry points over the equivalent
-identity tables; the paged route's own parity against the oracle (and, for
-one f16 sequence, against the reference's flash route) is tested in
-test_gpu_parity.py."""
+"""Decode on contiguous caches (emelk_attn_decode_contiguous): each
+sequence's pages in order, no block table.  The kernel is the paged one with
+the page of a token computed instead of read, so every result must equal,
+bit for bit, the paged entry points over the equivalent identity tables (the
+paged route's own parity against the oracle is tested in
+test_gpu_parity.py).  With one page spanning the capacity the pools are the
+flash route's caches (make_flash_attn_request, text/generator/detail.hpp:
+3232-3292), which the last test passes as they are."""
 import numpy as np
 import pytest
 
@@ -94,3 +94,53 @@ def test_contiguous_decode_append_equals_paged_decode_append(device, case):
     torch.cuda.synchronize()
     assert torch.equal(out_a.view(torch.int32), out_b.view(torch.int32))
     assert torch.equal(sc_a.k_pool, sc_b.k_pool) and torch.equal(sc_a.v_pool, sc_b.v_pool)
+
+
+@pytest.mark.parametrize("cap,n,D,G", [(640, 513, 128, 2), (96, 1, 128, 2), (1024, 1000, 64, 4)])
+def test_contiguous_decode_on_the_flash_route_caches(device, cap, n, D, G):
+    """The reference's flash caches, [layer][kv_head][capacity][head_dim] f16
+    (make_flash_attn_request's src1/src2 views, text/generator/detail.hpp:
+    3258-3269), are the pool of a geometry with block_tokens = capacity and
+    max_blocks = 1: passed as they are, the step stores its token at n - 1
+    and attends over n tokens, held to the bar against the reference's flash
+    route (f16 accumulator) and the fp64 ideal."""
+    import torch
+    import oracle
+    from kvsetup import assert_close
+    banner(f"contiguous decode on flash-layout caches cap={cap} n={n} D={D} G={G}")
+    L, HK = 2, 4
+    H = HK * G
+    g = emelk.geometry(L, H, HK, D, cap, 1)
+    rng = np.random.default_rng(cap + n)
+    k16 = oracle.fp32_to_fp16(rng.standard_normal((L, HK, cap, D)).astype(np.float32))
+    v16 = oracle.fp32_to_fp16(rng.standard_normal((L, HK, cap, D)).astype(np.float32))
+    assert emelk.pool_bytes(g) == k16.nbytes
+    k_pool = torch.from_numpy(k16.view(np.uint8).ravel().copy()).to(device)
+    v_pool = torch.from_numpy(v16.view(np.uint8).ravel().copy()).to(device)
+    layer = 1
+    q = rng.standard_normal((1, H * D)).astype(np.float32)
+    nk = rng.standard_normal((1, HK * D)).astype(np.float32)
+    nv = rng.standard_normal((1, HK * D)).astype(np.float32)
+    qd = torch.from_numpy(q).to(device).view(1, H, D)
+    out = torch.full_like(qd, float("nan"))
+    ws = torch.zeros(emelk.decode_workspace_bytes(g, 1, n) // 4 + 1, dtype=torch.float32,
+                     device=device)
+    kl = torch.tensor([n], dtype=torch.int32, device=device)
+    scale = float(1.0 / np.sqrt(D))
+    emelk.decode_contiguous(g, k_pool, v_pool, layer, qd, out, kl, n, cap, scale, ws,
+                            k_rows=torch.from_numpy(nk).to(device),
+                            v_rows=torch.from_numpy(nv).to(device))
+    torch.cuda.synchronize()
+    got = out.view(-1).cpu().numpy()
+    # the store: row n - 1 of every head holds fp16 of the new rows
+    k16[layer, :, n - 1] = oracle.fp32_to_fp16(nk.reshape(HK, D))
+    v16[layer, :, n - 1] = oracle.fp32_to_fp16(nv.reshape(HK, D))
+    assert np.array_equal(k_pool.cpu().numpy(), k16.view(np.uint8).ravel())
+    assert np.array_equal(v_pool.cpu().numpy(), v16.view(np.uint8).ravel())
+    flash = oracle.flash_attn_f16acc(q[0], np.ascontiguousarray(k16[layer]),
+                                     np.ascontiguousarray(v16[layer]), D, H, HK, n, cap, scale)
+    assert_close(got, flash, what="vs the reference's flash route (f16 accumulator)")
+    rows = lambda x: oracle.fp16_to_fp32(x[layer, :, :n].transpose(1, 0, 2).reshape(n, HK * D))  # noqa: E731
+    qr = oracle.fp16_to_fp32(oracle.fp32_to_fp16(q[0]))
+    ideal = oracle.attention_f64(qr, rows(k16), rows(v16), H, HK, D, n, scale)
+    assert_close(got, ideal, what="vs fp64 ideal")
