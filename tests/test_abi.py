@@ -214,3 +214,15 @@ def test_python_helpers_reject_bad_tensors_before_any_launch():
                             F(torch.zeros(2, dtype=torch.int32)), tables, 0.125)
     with pytest.raises(ValueError):
         emelk.copy_blocks(g, kp, vp, F(torch.zeros(4, 3, dtype=torch.int32)))
+    # contiguous decode: the same tensor checks, and its stored rows come in pairs
+    krow = F(torch.zeros(3, 2 * 64))
+    for case in cases[:7] + [dict(workspace=None)]:
+        a = dict(base, **case)
+        with pytest.raises((ValueError, TypeError)):
+            emelk.decode_contiguous(g, a["k_pool"], a["v_pool"], 0, a["q"], a["out"],
+                                    a["kv_lens"], 10, 16, 0.125, a["workspace"])
+    with pytest.raises(ValueError):
+        emelk.decode_contiguous(g, kp, vp, 0, q, out, lens, 10, 16, 0.125, ws, k_rows=krow)
+    with pytest.raises(ValueError):
+        emelk.decode_contiguous(g, kp, vp, 0, q, out, lens, 10, 16, 0.125, ws, k_rows=krow,
+                                v_rows=F(torch.zeros(3, 64)))
