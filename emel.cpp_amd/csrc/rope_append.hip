@@ -14,8 +14,10 @@
 //
 // Launch: one workgroup of 4 waves per (token, group of 4 rows), where the
 // rows of a token are its n_head q heads, n_head_kv k heads and n_head_kv v
-// heads.  A wave stages its row of head_dim floats in LDS.  This is a few KB
-// per token: latency, not bandwidth, bounds it.
+// heads.  A wave stages its row of head_dim floats in its own slice of LDS,
+// so it needs no workgroup barrier, and requests the row together with the
+// token's position.  This is a few KB per token: latency, not bandwidth,
+// bounds it.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -79,17 +81,6 @@ __global__ __launch_bounds__(k_rows_per_wg *k_wave) void rope_append_kernel(rope
   const int32_t D = L.head_dim;
   const int32_t s = blockIdx.x / A.n_tokens;
   const int32_t t = blockIdx.x % A.n_tokens;
-  const int32_t pos = A.positions[s] + t;
-  // Token validity is uniform over the workgroup, so the early exit keeps
-  // every barrier below uniform.
-  if (pos < 0) return;
-  if (A.pair_count > 0 && pos >= A.rope_positions) return;
-  const int32_t lb = pos / L.block_tokens;
-  if (lb >= A.table_stride) return;
-  const uint32_t page = A.tables[static_cast<uint64_t>(s) * A.table_stride + lb];
-  if (page >= static_cast<uint32_t>(L.max_blocks)) return;
-  const int32_t slot = pos % L.block_tokens;
-
   const int32_t wave = threadIdx.x / k_wave;
   const int32_t lane = threadIdx.x % k_wave;
   const int32_t row = blockIdx.y * k_rows_per_wg + wave;
@@ -98,24 +89,59 @@ __global__ __launch_bounds__(k_rows_per_wg *k_wave) void rope_append_kernel(rope
   const int32_t kind = row < L.n_head ? 0 : (row < L.n_head + L.n_head_kv ? 1 : 2);
   const int32_t head = kind == 0 ? row : (kind == 1 ? row - L.n_head : row - L.n_head - L.n_head_kv);
   const uint64_t tok = static_cast<uint64_t>(s) * A.n_tokens + t;
-  const float *src = nullptr;
+  // The row is requested together with the position (two floats per lane
+  // per 128 dims), before the token's validity is known.
+  constexpr int NC = k_max_dim / (2 * k_wave);
+  float2 x[NC];
   if (have) {
-    if (kind == 0) {
-      src = A.q_in + (tok * L.n_head + head) * static_cast<uint64_t>(D);
-    } else {
-      src = (kind == 1 ? A.k_rows : A.v_rows) + (tok * L.n_head_kv + head) * static_cast<uint64_t>(D);
+    const float *src =
+        kind == 0 ? A.q_in + (tok * L.n_head + head) * static_cast<uint64_t>(D)
+                  : (kind == 1 ? A.k_rows : A.v_rows) + (tok * L.n_head_kv + head) * static_cast<uint64_t>(D);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int32_t d = 2 * (lane + c * k_wave);
+      if (d < D) x[c] = *reinterpret_cast<const float2 *>(src + d);
     }
   }
-  float *buf = s_row[wave];
-  if (have) {
-    for (int32_t d = lane; d < D; d += k_wave) buf[d] = src[d];
+  const int32_t pos = A.positions[s] + t;
+  // An invalid token (no position, outside the rope table, past the table
+  // row or on an invalid page) writes nothing, q included.
+  if (pos < 0) return;
+  if (A.pair_count > 0 && pos >= A.rope_positions) return;
+  // the (cos, sin) of the lane's pairs, requested with the page
+  constexpr int NP = k_max_dim / (2 * k_wave);
+  float2 cs[NP];
+  if (have && kind < 2) {
+#pragma unroll
+    for (int c = 0; c < NP; ++c) {
+      const int32_t pr = lane + c * k_wave;
+      if (pr < A.pair_count) cs[c] = A.rope[static_cast<uint64_t>(pos) * A.pair_count + pr];
+    }
   }
-  __syncthreads();
+  const int32_t lb = pos / L.block_tokens;
+  if (lb >= A.table_stride) return;
+  const uint32_t page = A.tables[static_cast<uint64_t>(s) * A.table_stride + lb];
+  if (page >= static_cast<uint32_t>(L.max_blocks)) return;
+  const int32_t slot = pos % L.block_tokens;
+  if (!have) return;  // uniform per wave; nothing below synchronises across waves
+  // Each wave stages only its own row (and its s_scale), so ordering its
+  // own LDS operations is all the synchronisation needed.
+  auto wave_sync = []() {
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+  };
+  float *buf = s_row[wave];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int32_t d = 2 * (lane + c * k_wave);
+    if (d < D) *reinterpret_cast<float2 *>(buf + d) = x[c];
+  }
+  wave_sync();
 
   // Norm scale, computed by one lane in the reference's summation order.
   const float *wt = kind == 0 ? A.q_norm : (kind == 1 ? A.k_norm : nullptr);
-  const bool head_norm = have && kind < 2 && wt != nullptr;
-  const bool v_norm = have && kind == 2 && A.v_rms != 0;
+  const bool head_norm = kind < 2 && wt != nullptr;
+  const bool v_norm = kind == 2 && A.v_rms != 0;
   if (lane == 0 && head_norm) {
     // apply_headwise_rms_norm (detail.hpp:1073-1082)
     float ss = 0.0f;
@@ -163,35 +189,41 @@ __global__ __launch_bounds__(k_rows_per_wg *k_wave) void rope_append_kernel(rope
     const float mean = static_cast<float>(ss / static_cast<double>(n));
     if (lane == 0) s_scale[wave] = 1.0f / sqrtf(mean + A.eps);
   }
-  __syncthreads();
-  if (head_norm) {
-    const float inv = s_scale[wave];
-    for (int32_t d = lane; d < D; d += k_wave) buf[d] *= inv * wt[d];
-  } else if (v_norm) {
+  if (head_norm || v_norm) {
+    wave_sync();
     const float sc = s_scale[wave];
-    for (int32_t d = lane; d < D; d += k_wave) buf[d] *= sc;
+    if (head_norm) {
+      for (int32_t d = lane; d < D; d += k_wave) buf[d] *= sc * wt[d];
+    } else {
+      for (int32_t d = lane; d < D; d += k_wave) buf[d] *= sc;
+    }
+    wave_sync();
   }
-  __syncthreads();
 
   // apply_rope_pairing (detail.hpp:2905-2936): lane p rotates pairs p,
   // p + 64, ... (pairs never overlap, so the order does not matter)
-  if (have && kind < 2) {
-    for (int32_t pr = lane; pr < A.pair_count; pr += k_wave) {
+  if (kind < 2 && A.pair_count > 0) {
+#pragma unroll
+    for (int c = 0; c < NP; ++c) {
+      const int32_t pr = lane + c * k_wave;
+      if (pr >= A.pair_count) break;
       const int32_t d0 = pr * A.x0_stride;
       const int32_t d1 = pr * A.x1_stride + A.x1_base;
-      const float2 cs = A.rope[static_cast<uint64_t>(pos) * A.pair_count + pr];
       const float x0 = buf[d0];
       const float x1 = buf[d1];
-      buf[d0] = x0 * cs.x - x1 * cs.y;
-      buf[d1] = x0 * cs.y + x1 * cs.x;
+      buf[d0] = x0 * cs[c].x - x1 * cs[c].y;
+      buf[d1] = x0 * cs[c].y + x1 * cs[c].x;
     }
+    wave_sync();
   }
-  __syncthreads();
-  if (!have) return;
 
   if (kind == 0) {
     float *dst = A.q_out + (tok * L.n_head + head) * static_cast<uint64_t>(D);
-    for (int32_t d = lane; d < D; d += k_wave) dst[d] = buf[d];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int32_t d = 2 * (lane + c * k_wave);
+      if (d < D) *reinterpret_cast<float2 *>(dst + d) = *reinterpret_cast<const float2 *>(buf + d);
+    }
     return;
   }
   uint8_t *region = (kind == 1 ? A.k_pool : A.v_pool) +
