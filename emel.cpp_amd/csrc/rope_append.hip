@@ -46,6 +46,13 @@ namespace {
 using namespace emelk::dev;
 
 constexpr int k_rows_per_wg = 4;
+// rope_append_rows_kernel: rows per wave, and the launch size (rows) from
+// which it replaces rope_append_kernel
+#ifndef EMELK_ROPE_RPW
+#define EMELK_ROPE_RPW 4
+#endif
+constexpr int k_rows_per_wave = EMELK_ROPE_RPW;
+constexpr int64_t k_rows_kernel_min = 1 << 16;
 constexpr int k_max_dim = 512;
 
 struct rope_append_args {
@@ -57,6 +64,7 @@ struct rope_append_args {
   float *q_out;
   const float *k_rows;
   const float *v_rows;
+  int32_t n_seq;
   int32_t n_tokens;
   const int32_t *positions;
   const uint16_t *tables;
@@ -248,6 +256,205 @@ __global__ __launch_bounds__(k_rows_per_wg *k_wave) void rope_append_kernel(rope
   }
 }
 
+// Large launches (a prefill chunk): each wave takes RPW consecutive
+// (token, row) pairs, token-major, and requests all of their rows and
+// positions, then all of their pages and (cos, sin), before it stages any
+// row, so a wave keeps RPW rows in flight instead of one.  Every loop over
+// the rows is unrolled (the per-row registers stay registers), the page is
+// read as the aligned 32-bit word that holds it (a scalar load, which does
+// not wait behind the row loads), and the arithmetic per row is that of
+// rope_append_kernel.
+// REG: adjacent pairs (d, d + 1), no norms, f16 pool: a lane's two floats
+// are exactly its pair, so the row never leaves registers.
+template <int D, int RPW, bool REG>
+__global__ __launch_bounds__(k_rows_per_wg *k_wave) void rope_append_rows_kernel(rope_append_args A) {
+  __shared__ __align__(16) float s_row[k_rows_per_wg][D];  // float4 reads (q8_0)
+  __shared__ float s_scale[k_rows_per_wg];
+  constexpr int NC = D / (2 * k_wave) > 0 ? D / (2 * k_wave) : 1;  // float2 per lane per row
+  const pool_layout &L = A.L;
+  const int32_t wave = __builtin_amdgcn_readfirstlane(static_cast<int32_t>(threadIdx.x / k_wave));
+  const int32_t lane = threadIdx.x % k_wave;
+  const uint32_t n_rows = static_cast<uint32_t>(L.n_head + 2 * L.n_head_kv);
+  const uint32_t n_tok = static_cast<uint32_t>(A.n_tokens);
+  const uint32_t total = static_cast<uint32_t>(A.n_seq) * n_tok * n_rows;  // < 2^31 (host check)
+  const uint32_t base = (blockIdx.x * k_rows_per_wg + static_cast<uint32_t>(wave)) * RPW;
+  float *buf = s_row[wave];
+  auto wave_sync = []() {
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+  };
+
+  uint32_t tok[RPW], seq[RPW];
+  int32_t kind[RPW], head[RPW], pos[RPW];
+  uint32_t page[RPW];
+  bool ok[RPW];
+  float2 x[RPW][NC], cs[RPW][NC];
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    const uint32_t gr = base + i < total ? base + i : total - 1;  // past the end: a valid address
+    tok[i] = gr / n_rows;
+    const int32_t row = static_cast<int32_t>(gr - tok[i] * n_rows);
+    kind[i] = row < L.n_head ? 0 : (row < L.n_head + L.n_head_kv ? 1 : 2);
+    head[i] = kind[i] == 0 ? row : (kind[i] == 1 ? row - L.n_head : row - L.n_head - L.n_head_kv);
+    const float *src = kind[i] == 0
+                           ? A.q_in + (static_cast<uint64_t>(tok[i]) * L.n_head + head[i]) * D
+                           : (kind[i] == 1 ? A.k_rows : A.v_rows) +
+                                 (static_cast<uint64_t>(tok[i]) * L.n_head_kv + head[i]) * D;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int32_t d = 2 * (lane + c * k_wave);
+      if (d < D) x[i][c] = *reinterpret_cast<const float2 *>(src + d);
+    }
+    seq[i] = tok[i] / n_tok;
+    pos[i] = A.positions[seq[i]] + static_cast<int32_t>(tok[i] - seq[i] * n_tok);
+  }
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    // An invalid token (no position, outside the rope table, past the table
+    // row or on an invalid page) writes nothing, q included.
+    bool v = base + i < total && pos[i] >= 0 &&
+             (A.pair_count == 0 || pos[i] < A.rope_positions);
+    const int32_t lb = v ? pos[i] / L.block_tokens : 0;
+    v = v && lb < A.table_stride;
+    const uintptr_t at = reinterpret_cast<uintptr_t>(
+        A.tables + static_cast<uint64_t>(seq[i]) * A.table_stride + lb);
+    const uint32_t w = *reinterpret_cast<const uint32_t *>(at & ~uintptr_t{3});
+    page[i] = v ? ((at & 2) ? (w >> 16) : (w & 0xFFFFu)) : 0xFFFFFFFFu;
+    ok[i] = page[i] < static_cast<uint32_t>(L.max_blocks);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int32_t pr = lane + c * k_wave;
+      if (v && kind[i] < 2 && pr < A.pair_count) {
+        cs[i][c] = A.rope[static_cast<uint64_t>(pos[i]) * A.pair_count + pr];
+      }
+    }
+  }
+  if constexpr (REG) {
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+      if (!ok[i]) continue;  // uniform
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int32_t pr = lane + c * k_wave;  // the lane's pair: dims 2 pr, 2 pr + 1
+        if (2 * pr >= D) continue;
+        float2 y = x[i][c];
+        if (kind[i] < 2 && pr < A.pair_count) {  // apply_rope_pairing, same expressions
+          const float x0 = y.x, x1 = y.y;
+          y.x = x0 * cs[i][c].x - x1 * cs[i][c].y;
+          y.y = x0 * cs[i][c].y + x1 * cs[i][c].x;
+        }
+        if (kind[i] == 0) {
+          *reinterpret_cast<float2 *>(A.q_out + (static_cast<uint64_t>(tok[i]) * L.n_head + head[i]) * D +
+                                      2 * pr) = y;
+        } else {
+          const int32_t slot = pos[i] % L.block_tokens;
+          uint8_t *region = (kind[i] == 1 ? A.k_pool : A.v_pool) +
+                            L.region_offset(A.layer, static_cast<int32_t>(page[i]), head[i]);
+          reinterpret_cast<uint32_t *>(region + static_cast<uint64_t>(slot) * D * 2u)[pr] =
+              as_u32(pack_half2(y.x, y.y));
+        }
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    if (ok[i]) {  // uniform
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int32_t d = 2 * (lane + c * k_wave);
+        if (d < D) *reinterpret_cast<float2 *>(buf + d) = x[i][c];
+      }
+      wave_sync();
+      const float *wt = kind[i] == 0 ? A.q_norm : (kind[i] == 1 ? A.k_norm : nullptr);
+      const bool head_norm = kind[i] < 2 && wt != nullptr;
+      const bool v_norm = kind[i] == 2 && A.v_rms != 0;
+      if (lane == 0 && head_norm) {
+        // apply_headwise_rms_norm (detail.hpp:1073-1082)
+        float ss = 0.0f;
+        for (int32_t d = 0; d < D; ++d) ss += buf[d] * buf[d];
+        s_scale[wave] = 1.0f / sqrtf(ss / static_cast<float>(D) + A.eps);
+      }
+      if (v_norm) {
+        // apply_rms_norm_in_place (detail.hpp:1098-1106), in the order of
+        // rope_append_kernel: one fp64 chain over the token's whole v
+        const float *vv = A.v_rows + static_cast<uint64_t>(tok[i]) * L.n_head_kv * D;
+        const int32_t n = L.n_head_kv * D;
+        double ss = 0.0;
+        for (int32_t c0 = 0; c0 < n; c0 += k_wave) {
+          const int32_t j = c0 + lane;
+          const float xv = j < n ? vv[j] : 0.0f;
+          const float sq = xv * xv;
+          const int32_t left = n - c0 < k_wave ? n - c0 : k_wave;
+          for (int32_t l = 0; l < left; ++l) {
+            ss += static_cast<double>(
+                __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sq), l)));
+          }
+        }
+        const float mean = static_cast<float>(ss / static_cast<double>(n));
+        if (lane == 0) s_scale[wave] = 1.0f / sqrtf(mean + A.eps);
+      }
+      if (head_norm || v_norm) {
+        wave_sync();
+        const float sc = s_scale[wave];
+        if (head_norm) {
+          for (int32_t d = lane; d < D; d += k_wave) buf[d] *= sc * wt[d];
+        } else {
+          for (int32_t d = lane; d < D; d += k_wave) buf[d] *= sc;
+        }
+        wave_sync();
+      }
+      // apply_rope_pairing (detail.hpp:2905-2936)
+      if (kind[i] < 2 && A.pair_count > 0) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const int32_t pr = lane + c * k_wave;
+          if (pr < A.pair_count) {
+            const int32_t d0 = pr * A.x0_stride;
+            const int32_t d1 = pr * A.x1_stride + A.x1_base;
+            const float x0 = buf[d0];
+            const float x1 = buf[d1];
+            buf[d0] = x0 * cs[i][c].x - x1 * cs[i][c].y;
+            buf[d1] = x0 * cs[i][c].y + x1 * cs[i][c].x;
+          }
+        }
+        wave_sync();
+      }
+      if (kind[i] == 0) {
+        float *dst = A.q_out + (static_cast<uint64_t>(tok[i]) * L.n_head + head[i]) * D;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const int32_t d = 2 * (lane + c * k_wave);
+          if (d < D) *reinterpret_cast<float2 *>(dst + d) = *reinterpret_cast<const float2 *>(buf + d);
+        }
+      } else {
+        const int32_t slot = pos[i] % L.block_tokens;
+        uint8_t *region = (kind[i] == 1 ? A.k_pool : A.v_pool) +
+                          L.region_offset(A.layer, static_cast<int32_t>(page[i]), head[i]);
+        if (L.kv_type == EMELK_KV_F16) {
+          // store_fp16_rounded_cache (detail.hpp:3050-3055): RNE per value
+          uint32_t *dst = reinterpret_cast<uint32_t *>(region + static_cast<uint64_t>(slot) * D * 2u);
+          for (int32_t j = lane; j < D / 2; j += k_wave) dst[j] = as_u32(pack_half2(buf[2 * j], buf[2 * j + 1]));
+        } else {
+          constexpr int32_t blocks = D / 32;
+          if (lane < blocks) {
+            int8_t qs[32];
+            uint16_t dq;
+            quantize_block32(buf + 32 * lane, qs, dq);
+            uint4_t *dst = reinterpret_cast<uint4_t *>(region + static_cast<uint64_t>(slot) * D +
+                                                       static_cast<uint64_t>(lane) * 32u);
+            dst[0] = __builtin_bit_cast(uint4_t, *reinterpret_cast<int8_t(*)[16]>(qs));
+            dst[1] = __builtin_bit_cast(uint4_t, *reinterpret_cast<int8_t(*)[16]>(qs + 16));
+            reinterpret_cast<uint16_t *>(region + L.scale_plane())[static_cast<uint64_t>(slot) * blocks +
+                                                                   lane] = dq;
+          }
+        }
+      }
+      wave_sync();  // the next row reuses buf
+    }
+  }
+}
+
 // Checks a pairing: every pair inside the head and no dim used twice.
 bool pairing_ok(const emelk_rope_params &p, int32_t head_dim, int32_t pair_count, int32_t x1_base) {
   if (p.x0_stride < 0 || p.x1_stride < 0 || x1_base < 0) return false;
@@ -365,6 +572,7 @@ extern "C" emel_error_type emelk_kv_qkv_rope_append(
   A.q_out = q_out;
   A.k_rows = k_rows;
   A.v_rows = v_rows;
+  A.n_seq = n_seq;
   A.n_tokens = n_tokens;
   A.positions = positions;
   A.tables = block_tables;
@@ -380,9 +588,34 @@ extern "C" emel_error_type emelk_kv_qkv_rope_append(
   A.v_rms = v_rms;
   A.eps = rms_epsilon;
   const int32_t n_rows = L.n_head + 2 * L.n_head_kv;
-  const dim3 grid(static_cast<uint32_t>(n_seq * n_tokens),
-                  static_cast<uint32_t>((n_rows + emelk::k_rows_per_wg - 1) / emelk::k_rows_per_wg));
-  hipLaunchKernelGGL(emelk::rope_append_kernel, grid, dim3(emelk::k_rows_per_wg * emelk::k_wave),
-                     0, static_cast<hipStream_t>(stream), A);
+  const int64_t rows = static_cast<int64_t>(n_seq) * n_tokens * n_rows;
+  const dim3 block(emelk::k_rows_per_wg * emelk::k_wave);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (rows >= emelk::k_rows_kernel_min && rows < 0x7FFFFFFF) {
+    constexpr int RPW = emelk::k_rows_per_wave;
+    constexpr int64_t per_wg = emelk::k_rows_per_wg * RPW;
+    const dim3 grid(static_cast<uint32_t>((rows + per_wg - 1) / per_wg));
+    const bool reg = L.kv_type == EMELK_KV_F16 && q_norm == nullptr && k_norm == nullptr &&
+                     v_rms == 0 && A.x0_stride == 2 && A.x1_stride == 2 && A.x1_base == 1;
+    if (reg) {
+      switch (L.head_dim) {
+        case 64: hipLaunchKernelGGL((emelk::rope_append_rows_kernel<64, RPW, true>), grid, block, 0, st, A); break;
+        case 128: hipLaunchKernelGGL((emelk::rope_append_rows_kernel<128, RPW, true>), grid, block, 0, st, A); break;
+        case 256: hipLaunchKernelGGL((emelk::rope_append_rows_kernel<256, RPW, true>), grid, block, 0, st, A); break;
+        default: hipLaunchKernelGGL((emelk::rope_append_rows_kernel<512, RPW, true>), grid, block, 0, st, A); break;
+      }
+    } else {
+      switch (L.head_dim) {
+        case 64: hipLaunchKernelGGL((emelk::rope_append_rows_kernel<64, RPW, false>), grid, block, 0, st, A); break;
+        case 128: hipLaunchKernelGGL((emelk::rope_append_rows_kernel<128, RPW, false>), grid, block, 0, st, A); break;
+        case 256: hipLaunchKernelGGL((emelk::rope_append_rows_kernel<256, RPW, false>), grid, block, 0, st, A); break;
+        default: hipLaunchKernelGGL((emelk::rope_append_rows_kernel<512, RPW, false>), grid, block, 0, st, A); break;
+      }
+    }
+  } else {
+    const dim3 grid(static_cast<uint32_t>(n_seq * n_tokens),
+                    static_cast<uint32_t>((n_rows + emelk::k_rows_per_wg - 1) / emelk::k_rows_per_wg));
+    hipLaunchKernelGGL(emelk::rope_append_kernel, grid, block, 0, st, A);
+  }
   return hipGetLastError() == hipSuccess ? EMELK_ERR_NONE : EMELK_ERR_BACKEND;
 }

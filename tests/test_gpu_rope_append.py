@@ -22,6 +22,15 @@ CASES = [
     (emelk.KV_F16, 32, 8, 64, 16, emelk.NORMAL_PAIRING, 64, 5e5, False, False, [33, 1, 47]),
     (emelk.KV_Q8_0, 32, 8, 128, 32, emelk.NORMAL_PAIRING, 128, 5e5, False, False, [65, 40]),
     (emelk.KV_Q8_0, 8, 2, 128, 32, emelk.NEOX_PAIRING, 64, 1e4, True, True, [37, 96]),
+    # launches of 65536 rows or more (prefill chunks) take the multi-row
+    # kernel: its register route (adjacent pairs, no norms, f16; two
+    # sequences whose table rows start 2 bytes off a 4-byte boundary, since
+    # the stride of 45 pages is odd) and its LDS route
+    (emelk.KV_F16, 32, 8, 128, 32, emelk.NORMAL_PAIRING, 128, 5e5, False, False, [1370, 1370]),
+    (emelk.KV_F16, 32, 8, 64, 16, emelk.NORMAL_PAIRING, 32, 5e5, False, False, [1400]),
+    (emelk.KV_F16, 16, 8, 128, 32, emelk.NEOX_PAIRING, 128, 1e6, True, False, [2100]),
+    (emelk.KV_Q8_0, 32, 8, 128, 32, emelk.NORMAL_PAIRING, 128, 5e5, False, False, [1400]),
+    (emelk.KV_Q8_0, 8, 2, 128, 32, emelk.NEOX_PAIRING, 64, 1e4, True, True, [5500]),
 ]
 
 
@@ -135,6 +144,49 @@ def test_qkv_rope_append_skips_tokens_outside_table_and_pool(device):
                           v[:, :1], pos, bad, rope)
     torch.cuda.synchronize()
     assert np.all(q_out.cpu().numpy()[0, 0] == 7.0)
+    rope.close()
+
+
+def test_qkv_rope_append_skips_in_a_multi_row_launch(device):
+    """The same skips in a launch of 65536 rows or more (the multi-row
+    kernel): tokens past the rope table, and the tokens of an invalid page,
+    write neither q nor the pool; every other token is bit-exact."""
+    import torch
+    banner("qkv_rope_append skips, multi-row launch")
+    n, H, HK, D, bt = 1400, 32, 8, 64, 16
+    sc = Scenario(n_layer=1, n_head=H, n_kv=HK, head_dim=D, block_tokens=bt, lens=[n], seed=8,
+                  fill=False)
+    assert n * (H + 2 * HK) >= 65536
+    rope = emelk.RopeTable(D, D, 1000, 1e4)  # positions [0, 1000) only
+    bad = sc.tables.clone()
+    bad[0, 3] = -1  # tokens 48..63: an invalid page
+    rng = np.random.default_rng(9)
+    q = rng.standard_normal((n, H * D)).astype(np.float32)
+    q_out = torch.full((1, n, H * D), 7.0, device=device)
+    emelk.qkv_rope_append(sc.g, sc.k_pool, sc.v_pool, 0, torch.from_numpy(q).to(device).view(1, n, -1),
+                          q_out, torch.from_numpy(sc.k_rows[0][0]).to(device).view(1, n, -1),
+                          torch.from_numpy(sc.v_rows[0][0]).to(device).view(1, n, -1),
+                          torch.zeros(1, dtype=torch.int32, device=device), bad, rope)
+    torch.cuda.synchronize()
+    got = q_out.cpu().numpy()[0]
+    skipped = [t >= 1000 or t // bt == 3 for t in range(n)]
+    written = np.zeros((n, HK * D), bool)
+    for t in range(n):
+        if skipped[t]:
+            assert np.all(got[t] == 7.0), t
+            continue
+        qo, ko, vo = oracle.qkv_rope_rows(q[t], sc.k_rows[0][0][t], sc.v_rows[0][0][t], H, HK, D,
+                                          emelk.NORMAL_PAIRING, D, 1e4, t)
+        np.testing.assert_array_equal(got[t].view(np.uint32), qo.view(np.uint32), err_msg=str(t))
+        sc.k_rows[0][0][t], sc.v_rows[0][0][t] = ko, vo
+        written[t] = True
+    # the pool holds exactly the written tokens (expected_pool leaves the
+    # others' bytes at zero, as the pool started)
+    for which, pool in (("k", sc.k_pool), ("v", sc.v_pool)):
+        rows = sc.k_rows if which == "k" else sc.v_rows
+        rows[0][0] = np.where(written, rows[0][0], 0.0).astype(np.float32)
+        np.testing.assert_array_equal(pool.cpu().numpy(), sc.expected_pool(which),
+                                      err_msg=f"{which} pool")
     rope.close()
 
 
