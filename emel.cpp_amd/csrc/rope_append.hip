@@ -260,10 +260,8 @@ __global__ __launch_bounds__(k_rows_per_wg *k_wave) void rope_append_kernel(rope
 // (token, row) pairs, token-major, and requests all of their rows and
 // positions, then all of their pages and (cos, sin), before it stages any
 // row, so a wave keeps RPW rows in flight instead of one.  Every loop over
-// the rows is unrolled (the per-row registers stay registers), the page is
-// read as the aligned 32-bit word that holds it (a scalar load, which does
-// not wait behind the row loads), and the arithmetic per row is that of
-// rope_append_kernel.
+// the rows is unrolled (the per-row registers stay registers), and the
+// arithmetic per row is that of rope_append_kernel.
 // REG: adjacent pairs (d, d + 1), no norms, f16 pool: a lane's two floats
 // are exactly its pair, so the row never leaves registers.
 template <int D, int RPW, bool REG>
@@ -316,10 +314,8 @@ __global__ __launch_bounds__(k_rows_per_wg *k_wave) void rope_append_rows_kernel
              (A.pair_count == 0 || pos[i] < A.rope_positions);
     const int32_t lb = v ? pos[i] / L.block_tokens : 0;
     v = v && lb < A.table_stride;
-    const uintptr_t at = reinterpret_cast<uintptr_t>(
-        A.tables + static_cast<uint64_t>(seq[i]) * A.table_stride + lb);
-    const uint32_t w = *reinterpret_cast<const uint32_t *>(at & ~uintptr_t{3});
-    page[i] = v ? ((at & 2) ? (w >> 16) : (w & 0xFFFFu)) : 0xFFFFFFFFu;
+    page[i] = v ? static_cast<uint32_t>(A.tables[static_cast<uint64_t>(seq[i]) * A.table_stride + lb])
+                : 0xFFFFFFFFu;
     ok[i] = page[i] < static_cast<uint32_t>(L.max_blocks);
 #pragma unroll
     for (int c = 0; c < NC; ++c) {

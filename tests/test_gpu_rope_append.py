@@ -24,8 +24,8 @@ CASES = [
     (emelk.KV_Q8_0, 8, 2, 128, 32, emelk.NEOX_PAIRING, 64, 1e4, True, True, [37, 96]),
     # launches of 65536 rows or more (prefill chunks) take the multi-row
     # kernel: its register route (adjacent pairs, no norms, f16; two
-    # sequences whose table rows start 2 bytes off a 4-byte boundary, since
-    # the stride of 45 pages is odd) and its LDS route
+    # sequences, the second's table row 2 bytes off a 4-byte boundary as the
+    # stride of 45 pages is odd) and its LDS route
     (emelk.KV_F16, 32, 8, 128, 32, emelk.NORMAL_PAIRING, 128, 5e5, False, False, [1370, 1370]),
     (emelk.KV_F16, 32, 8, 64, 16, emelk.NORMAL_PAIRING, 32, 5e5, False, False, [1400]),
     (emelk.KV_F16, 16, 8, 128, 32, emelk.NEOX_PAIRING, 128, 1e6, True, False, [2100]),
