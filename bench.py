@@ -104,6 +104,9 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy 1 GiB device-to-device three times (the reference kernel "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
+    ap.add_argument("--launch-floor", type=int, default=0, metavar="N",
+                    help="only time a replayed HIP graph of N back-to-back one-element kernels "
+                         "(the launch floor of a step of N dependent launches)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the KV hot path shards by "
@@ -120,6 +123,30 @@ def main():
             b.copy_(a)
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration_bytes": 1 << 30, "copies": 3}))
+        return
+    if args.launch_floor > 0:
+        # each launch depends on the one before (same stream), as the
+        # decode + combine launches of a step do
+        x = torch.zeros(1, dtype=torch.float32, device=dev)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(graph, stream=side):
+                for _ in range(args.launch_floor):
+                    x.add_(1.0)
+        torch.cuda.current_stream().wait_stream(side)
+        for _ in range(max(1, args.warmup)):
+            graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            graph.replay()
+        torch.cuda.synchronize()
+        ms = 1e3 * (time.perf_counter() - t0) / args.steps
+        print(json.dumps({"launch_floor_launches": args.launch_floor, "ms_per_graph": round(ms, 4),
+                          "us_per_launch": round(1e3 * ms / args.launch_floor, 3),
+                          "steps": args.steps}))
         return
     import emelk
 
