@@ -155,9 +155,15 @@ def main():
         result = run_config(args, torch, emelk, dev)
         if not args.headline_only:
             result["configs"] = other_configs(args, torch, emelk, dev)
-        print(json.dumps(result), flush=True)
-        return
-    print(json.dumps(run_config(args, torch, emelk, dev)), flush=True)
+    else:
+        result = run_config(args, torch, emelk, dev)
+    if TIMING_NOTES:
+        result["timing_notes"] = sorted(TIMING_NOTES)
+    print(json.dumps(result), flush=True)
+    bad = parity_failures(result)
+    if bad:
+        log(f"[bench] PARITY FAILED at {bad}")
+        sys.exit(3)
 
 
 PREFILL_CONFIGS = ("llama3-8b-prefill512-evict25", "llama3-8b-q8_0-prefill512-evict25",
@@ -191,14 +197,19 @@ def other_configs(args, torch, emelk, dev):
     return out
 
 
+TIMING_NOTES = set()
+
+
 def gpu_head_start(torch, cycles=40_000_000):
-    """Queue a spin kernel (tens of ms) ahead of an event-timed step, so the
-    host has enqueued the step's launches before the GPU reaches them: each
-    event interval then holds GPU time only, never host launch overhead."""
-    try:
-        torch.cuda._sleep(cycles)
-    except Exception:  # absent in some builds: intervals may then hold host gaps
-        pass
+    """Queue a spin kernel (tens of ms) ahead of an event-timed block, so the
+    host has enqueued the block's launches before the GPU reaches them: each
+    event interval then holds GPU time only, never host launch overhead.
+    False when this torch build has no spin kernel."""
+    sleep = getattr(torch.cuda, "_sleep", None)
+    if sleep is None:
+        return False
+    sleep(cycles)
+    return True
 
 
 def timed_blocks(torch, stream, launch, reps, prime=None):
@@ -206,13 +217,15 @@ def timed_blocks(torch, stream, launch, reps, prime=None):
     `stream`), `reps` times.  Each block is queued behind a spin kernel; a
     block whose launches were not all queued before the GPU reached its
     start event (the host stalled, e.g. freeing a large array) may hold host
-    gaps and is measured again.  `prime()`, queued between the spin and the
-    start event, runs untimed work first, so the timed block does not start
-    on a GPU that has just idled in the spin (its clocks ramp back up)."""
+    gaps and is measured again.  Without a spin kernel every interval is
+    kept and the line says that they may hold host gaps.  `prime()`, queued
+    between the spin and the start event, runs untimed work first, so the
+    timed block does not start on a GPU that has just idled in the spin (its
+    clocks ramp back up)."""
     times, tries = [], 0
     while len(times) < reps and tries < 4 * reps:
         tries += 1
-        gpu_head_start(torch)
+        spun = gpu_head_start(torch)
         if prime is not None:
             prime()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -221,11 +234,55 @@ def timed_blocks(torch, stream, launch, reps, prime=None):
         e1.record(stream)
         ahead = not e0.query()  # the GPU was still spinning when the last call was queued
         torch.cuda.synchronize()
-        if ahead:
+        if not spun:
+            TIMING_NOTES.add("no spin kernel in this torch build: event intervals may hold "
+                             "host launch gaps")
+        if ahead or not spun:
             times.append(e0.elapsed_time(e1))
     if not times:
         raise RuntimeError("could not queue a timed block ahead of the GPU")
     return times
+
+
+def graph_event_ms(torch, graph, stream, reps):
+    """HIP event time (ms) per replay of a captured graph, replayed `reps`
+    times back to back between one event pair on `stream` (no host gap can
+    fall between the graph's kernels)."""
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def parity_failures(obj, path=""):
+    """Paths of every `within_tolerance: false` in a result."""
+    bad = []
+    if isinstance(obj, dict):
+        for k, v in obj.items():
+            if k == "within_tolerance" and v is False:
+                bad.append(path or "/")
+            else:
+                bad += parity_failures(v, f"{path}/{k}")
+    elif isinstance(obj, list):
+        for i, v in enumerate(obj):
+            bad += parity_failures(v, f"{path}/{i}")
+    return bad
+
+
+def baseline_threads(args, lanes):
+    """One thread per sequence lane (or per row lane of a chunk), up to the
+    host threads this process may use and the box's share of 16."""
+    if args.cpu_threads:
+        return args.cpu_threads
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count() or 1
+    return max(1, min(lanes, usable, 16))
 
 
 def cpu_info(threads):
@@ -413,21 +470,13 @@ def decode_run(args, torch, emelk, dev):
         step()
     torch.cuda.synchronize()
     eager_ms = 1e3 * (time.perf_counter() - t_start) / K
-    # Kernel timing: after a GPU head start, one HIP event pair on the
-    # kernels' stream around the L back-to-back decode calls of a step (the
-    # appends of --separate-append left out: their rows are already stored),
-    # averaged per call.  No host gap and no event packet sits between two
-    # calls, so the figure is the decode (+ combine) kernels' own time.
-    def decode_block():
-        for layer in range(L):
-            attend(layer, not args.separate_append)
-
-    attn_avg_ms = float(np.mean(timed_blocks(torch, stream, decode_block, K,
-                                             prime=None if args.no_prime else decode_block))) / L
-
-    # Step timing: the 32-layer step (96 launches) captured once as a HIP
-    # graph and replayed K times, as a serving loop would run it.
+    # Step timing: the L-layer step captured once as a HIP graph and replayed
+    # K times, as a serving loop would run it (host clock for ms_per_step).
+    # Kernel timing (roofline): one HIP event pair on the replay stream
+    # around K more back-to-back replays, per layer call: decode (with the
+    # fused store) + combine, nothing else in the graph, no host gap.
     graph_ms = None
+    attn_avg_ms = None
     if not args.eager:
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
@@ -444,6 +493,23 @@ def decode_run(args, torch, emelk, dev):
             graph.replay()
         torch.cuda.synchronize()
         graph_ms = 1e3 * (time.perf_counter() - t_start) / K
+        if not args.separate_append:
+            attn_avg_ms = graph_event_ms(torch, graph, side, K) / L
+    if attn_avg_ms is None:
+        # eager or --separate-append: one HIP event pair around the L
+        # back-to-back decode calls of a step after a GPU head start (the
+        # appends of --separate-append left out: their rows are stored)
+        def decode_block():
+            for layer in range(L):
+                attend(layer, not args.separate_append)
+
+        attn_avg_ms = float(np.mean(timed_blocks(
+            torch, stream, decode_block, K,
+            prime=None if args.no_prime else decode_block))) / L
+    timing_basis = ("HIP events around K replays of the step's graph, per layer call"
+                    if graph_ms is not None and not args.separate_append else
+                    "HIP events around the L eager decode calls of a step after a GPU head "
+                    "start, per call")
     ms_per_step = graph_ms if graph_ms is not None else eager_ms
 
     # ---- algorithmic bytes ----
@@ -467,18 +533,15 @@ def decode_run(args, torch, emelk, dev):
     split = kernel_split(args, torch, step, ["decode_kernel", "combine_kernel", "append_f16_kernel",
                                              "append_q8_0_kernel"])
 
-    # ---- full-size parity check + CPU baseline ----
-    # f16: the oracle's restatement of compute_attention over every sequence
-    # of whole layers, on host threads, layer after layer until the CPU
-    # budget is spent; every layer's GPU output of the last step is checked.
-    # q8_0: the oracle's q8_0 route, one thread, sequence after sequence of
-    # layer 0 until the budget is spent.
+    # ---- full-size parity check + CPU baseline (oracle built -O3
+    # -march=native on this host) ----
     parity = None
     cpu = None
     if not args.no_cpu_baseline and contiguous:
         # the reference's route for an identity map: the flash decode with an
         # f16 accumulator (kernel/detail.hpp:5238-5291), one thread, every layer
         import oracle
+        nlib, build = oracle.native_lib()
         lb = pool_bytes // L
         worst, within, secs = 0.0, True, 0.0
         n = int(lens[0])
@@ -491,7 +554,8 @@ def decode_run(args, torch, emelk, dev):
                 heads.append(np.ascontiguousarray(h[:, :n]))
             qh = q[layer].view(B, H * D).cpu().numpy()
             t1 = time.perf_counter()
-            want = oracle.flash_attn_f16acc(qh[0], heads[0], heads[1], D, H, HK, n, n, scale)
+            want = oracle.flash_attn_f16acc(qh[0], heads[0], heads[1], D, H, HK, n, n, scale,
+                                            lib_=nlib)
             secs += time.perf_counter() - t1
             got = out[layer].view(B, H * D).cpu().numpy()[0]
             err = np.abs(got.astype(np.float64) - want)
@@ -501,27 +565,28 @@ def decode_run(args, torch, emelk, dev):
                   "max_abs_err": worst, "within_tolerance": within}
         cpu_step_s = secs
         cpu = {"value": round(step_kv_bytes / cpu_step_s / 1e9, 4), "unit": "GB/s",
-               **cpu_info(1), "kind": "port",
+               **cpu_info(1), "kind": "port", "build": build,
                "sample": f"all {L} layers of the step ({secs:.3f}s); oracle restatement of the "
-                         "flash route with an f16 accumulator, 1 thread",
+                         "flash route with an f16 accumulator, 1 thread (one sequence lane)",
                "steps_per_s": round(1.0 / cpu_step_s, 4)}
-    elif not args.no_cpu_baseline and kv_type == emelk.KV_F16:
+    elif not args.no_cpu_baseline:
+        # the reference route (compute_attention; the oracle's q8_0 route for
+        # q8_0 pools) over every sequence of whole layers, one thread per
+        # sequence lane, layer after layer until the CPU budget is spent;
+        # every layer's GPU output of the last step is checked
         import oracle
-        nthreads = args.cpu_threads or min(16, os.cpu_count() or 1)
-        lb = pool_bytes // L
+        nlib, build = oracle.native_lib()
+        nthreads = baseline_threads(args, B)
+        kind = "f16" if kv_type == emelk.KV_F16 else "q8_0"
         worst, within, secs, layers_done = 0.0, True, 0.0, 0
         for layer in range(L):
-            kp = k_pool[layer * lb:(layer + 1) * lb].cpu().numpy().view(np.uint16)
-            vp = v_pool[layer * lb:(layer + 1) * lb].cpu().numpy().view(np.uint16)
-            # pool [page][kv_head][t][D] -> reference token-major [page*bt + t][kv_head*D]
-            kc = np.ascontiguousarray(kp.reshape(max_blocks, HK, BT, D).transpose(0, 2, 1, 3)
-                                      ).reshape(max_blocks * BT, HK * D)
-            vc = np.ascontiguousarray(vp.reshape(max_blocks, HK, BT, D).transpose(0, 2, 1, 3)
-                                      ).reshape(max_blocks * BT, HK * D)
-            del kp, vp
+            kc, vc = (pool_token_major(p_, layer, L, max_blocks, HK, BT, D,
+                                       kv_type == emelk.KV_Q8_0, oracle)
+                      for p_ in (k_pool, v_pool))
             qh = q[layer].view(B, H * D).cpu().numpy()
-            want, t_layer = oracle.decode_batch_f16(qh, kc, vc, tables_h, lens, BT, H, HK, D,
-                                                    int(lens.max()), scale, nthreads)
+            want, t_layer = oracle.attention_rows(kind, qh, kc, vc, tables_h, lens, BT, H, HK, D,
+                                                  scale, nthreads, n_ctx=int(lens.max()),
+                                                  lib_=nlib)
             del kc, vc
             got = out[layer].view(B, H * D).cpu().numpy()
             err = np.abs(got.astype(np.float64) - want)
@@ -535,41 +600,11 @@ def decode_run(args, torch, emelk, dev):
                   "within_tolerance": within}
         cpu_step_s = secs / layers_done * L  # sample = whole layers; scaled to L layers
         cpu = {"value": round(step_kv_bytes / cpu_step_s / 1e9, 4), "unit": "GB/s",
-               **cpu_info(nthreads), "kind": "port",
+               **cpu_info(nthreads), "kind": "port", "build": build,
                "sample": f"{layers_done} layer(s) x {B} sequences of the same step "
                          f"({secs:.2f}s wall), scaled to {L} layers; oracle restatement of "
-                         f"compute_attention, {nthreads} threads",
-               "steps_per_s": round(1.0 / cpu_step_s, 6)}
-    elif not args.no_cpu_baseline:
-        import oracle
-        layer = 0
-        kc, vc = (pool_token_major(p_, layer, L, max_blocks, HK, BT, D, True, oracle)
-                  for p_ in (k_pool, v_pool))
-        order = np.random.default_rng(args.seed + 1).permutation(B).tolist()
-        qh = q[layer].view(B, H * D).cpu().numpy()
-        got = out[layer].view(B, H * D).cpu().numpy()
-        errs, t_cpu, pick = [], 0.0, []
-        for s in order:
-            t1 = time.perf_counter()
-            want = oracle.compute_attention_q8_0(qh[s], kc, vc, tables_h[s], BT, H, HK, D,
-                                                 int(lens[s]), int(lens[s]), scale)
-            t_cpu += time.perf_counter() - t1
-            pick.append(s)
-            errs.append((np.abs(got[s].astype(np.float64) - want),
-                         2e-3 + 1e-2 * np.abs(want.astype(np.float64))))
-            if t_cpu >= args.cpu_budget:
-                break
-        del kc, vc
-        parity = {"layer": layer, "n_sequences": len(pick), "sequences": sorted(pick)[:16],
-                  "max_abs_err": float(max(e.max() for e, _ in errs)),
-                  "within_tolerance": bool(all(np.all(e <= tol) for e, tol in errs))}
-        kv_done = float(sum(int(lens[s]) for s in pick))
-        cpu_step_s = t_cpu / kv_done * float(lens.sum()) * L  # per attended token, scaled
-        cpu = {"value": round(step_kv_bytes / cpu_step_s / 1e9, 4), "unit": "GB/s",
-               **cpu_info(1), "kind": "port",
-               "sample": f"{len(pick)} sequences x 1 layer of the step ({t_cpu:.2f}s), "
-                         f"scaled by attended tokens to {B} sequences x {L} layers; oracle q8_0 "
-                         "route, 1 thread",
+                         f"compute_attention ({kind} route), one thread per sequence lane, "
+                         f"{nthreads} threads",
                "steps_per_s": round(1.0 / cpu_step_s, 6)}
 
     metric = ("KV-read HBM GB/s (% of peak) + decode steps/s, 8B-shape b64 ctx8k"
@@ -611,6 +646,7 @@ def decode_run(args, torch, emelk, dev):
                                 (", emelk_attn_decode_contiguous (no block table)"
                                  if contiguous else "")),
                      "bytes_per_launch": kernel_bytes, "avg_launch_ms": round(attn_avg_ms, 4),
+                     "timing": timing_basis,
                      "decode_kernel_only": ({
                          "avg_launch_ms": dk["avg_ms"],
                          "achieved": round(kernel_bytes / (dk["avg_ms"] * 1e-3) / 1e9, 2),
@@ -618,7 +654,6 @@ def decode_run(args, torch, emelk, dev):
                                        4),
                          "source": "torch.profiler device trace of one eager step"}
                          if dk else None)},
-        "kernel_split": split,
         "cpu_baseline": cpu,
         "parity_full_size": parity,
     }
@@ -709,24 +744,36 @@ def prefill_evict(args, torch, emelk, dev):
             emelk.append(g, k_pool, v_pool, layer, ck[layer], cv[layer], qs, tables)
             emelk.prefill_chunk(g, k_pool, v_pool, layer, q[layer], out, qs, tables, scale)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    K = args.steps
-    t0 = time.perf_counter()
-    for k in range(K):
-        step()
-    torch.cuda.synchronize()
-    ms_step = 1e3 * (time.perf_counter() - t0) / K
-    # kernel timing: one HIP event pair around the L back-to-back chunk
-    # attention calls (the chunk rows are already appended), after a GPU
-    # head start, averaged per call
     def chunk_block():
         for layer in range(L):
             emelk.prefill_chunk(g, k_pool, v_pool, layer, q[layer], out, qs, tables, scale)
 
-    attn_ms = float(np.mean(timed_blocks(torch, stream, chunk_block, K,
-                                         prime=None if args.no_prime else chunk_block))) / L
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    K = args.steps
+    # Step: the L layers' append + chunk attention captured as one HIP graph
+    # and replayed K times (host clock).  Kernel timing (roofline): a graph
+    # of the L chunk-attention calls alone (the chunk rows are appended),
+    # replayed K times between one HIP event pair, per call.
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    g_step, g_attn = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g_step, stream=side):
+            step()
+        with torch.cuda.graph(g_attn, stream=side):
+            chunk_block()
+    torch.cuda.current_stream().wait_stream(side)
+    g_step.replay()
+    g_attn.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(K):
+        g_step.replay()
+    torch.cuda.synchronize()
+    ms_step = 1e3 * (time.perf_counter() - t0) / K
+    attn_ms = graph_event_ms(torch, g_attn, side, K) / L
     # bytes the kernel must move per launch: the unique K/V of the layer
     # (prefix + chunk, every KV head), the fp32 queries and the fp32 output
     prefill_bytes = (B * HK * (P0 + NQ) * (page_bytes // (HK * BT)) * 2
@@ -736,49 +783,54 @@ def prefill_evict(args, torch, emelk, dev):
     tflops = flops_layer / (attn_ms * 1e-3) / 1e12
 
     # parity sample + CPU baseline: the last layer's output (out is reused
-    # per layer) for 4 seeded (sequence, row) pairs against the oracle's
-    # per-row route (text/generator/detail.hpp:4297-4372), one thread
+    # per layer) for seeded (sequence, row) pairs against the oracle's
+    # per-row route (text/generator/detail.hpp:4297-4372), one thread per
+    # sequence lane, batches of rows until the CPU budget is spent
     parity = cpu = None
     if not args.no_cpu_baseline:
         import oracle
+        nlib, build = oracle.native_lib()
+        nthreads = baseline_threads(args, B)
         layer = L - 1
         kc, vc = (pool_token_major(p_, layer, L, max_blocks, HK, BT, D, q8, oracle)
                   for p_ in (k_pool, v_pool))
         tables_h = tables.cpu().numpy().view(np.uint16)
-        route = oracle.compute_attention_q8_0 if q8 else oracle.compute_attention_f16
         prng = np.random.default_rng(args.seed + 2)
         qh = q[layer].cpu().numpy()
         got = out.cpu().numpy()
         worst, ok_all, t_cpu, keys, pick = 0.0, True, 0.0, 0, []
         # seeded (sequence, row) pairs, the chunk's first and last rows
-        # first, until the CPU budget is spent (at least 4)
+        # first, two rows per thread per batch
         cand = [(0, 0), (B - 1, NQ - 1)] + [(int(prng.integers(B)), int(prng.integers(NQ)))
                                             for _ in range(4096)]
-        for s_, r_ in cand:
-            if len(pick) >= 4 and t_cpu >= args.cpu_budget:
+        per = 2 * nthreads
+        for i0 in range(0, len(cand), per):
+            if pick and t_cpu >= args.cpu_budget:
                 break
-            pick.append((s_, r_))
-            lim = P0 + r_ + 1
-            t1 = time.perf_counter()
-            want = route(qh[s_, r_].ravel(), kc, vc, tables_h[s_], BT, H, HK, D, lim, lim, scale)
-            t_cpu += time.perf_counter() - t1
-            keys += lim
-            e = np.abs(got[s_, r_].ravel().astype(np.float64) - want)
-            worst = max(worst, float(e.max()))
-            ok_all = ok_all and bool(np.all(e <= 2e-3 + 1e-2 * np.abs(want)))
+            batch = cand[i0:i0 + per]
+            lims = np.array([P0 + r_ + 1 for _, r_ in batch], np.int32)
+            qb = np.stack([qh[s_, r_].ravel() for s_, r_ in batch])
+            want, secs = oracle.attention_rows("q8_0" if q8 else "f16", qb, kc, vc, tables_h,
+                                               lims, BT, H, HK, D, scale, nthreads,
+                                               row_table=[s_ for s_, _ in batch], lib_=nlib)
+            t_cpu += secs
+            keys += int(lims.sum())
+            pick += batch
+            for j, (s_, r_) in enumerate(batch):
+                e = np.abs(got[s_, r_].ravel().astype(np.float64) - want[j])
+                worst = max(worst, float(e.max()))
+                ok_all = ok_all and bool(np.all(e <= 2e-3 + 1e-2 * np.abs(want[j])))
         parity = {"layer": layer, "n_rows": len(pick), "first_rows": pick[:6],
                   "max_abs_err": worst, "within_tolerance": ok_all}
         # the per-row route's time per attended key, scaled to a layer's keys
         layer_keys = B * float(np.sum(P0 + rows + 1))
         cpu_layer_s = t_cpu / keys * layer_keys
         cpu = {"value": round(flops_layer / cpu_layer_s / 1e12, 6), "unit": "TFLOP/s",
-               **cpu_info(1), "kind": "port",
-               "sample": f"{len(pick)} rows of layer {layer} ({t_cpu:.2f}s), scaled by attended "
-                         f"keys to the layer's {B * NQ} rows; oracle per-row route, 1 thread"}
+               **cpu_info(nthreads), "kind": "port", "build": build,
+               "sample": f"{len(pick)} rows of layer {layer} ({t_cpu:.2f}s wall), scaled by "
+                         f"attended keys to the layer's {B * NQ} rows; oracle per-row route, "
+                         f"one thread per sequence lane, {nthreads} threads"}
         del kc, vc
-
-    split = kernel_split(args, torch, step, ["prefill_kernel", "append_f16_kernel",
-                                             "append_q8_0_kernel", "decode_kernel"])
 
     # eviction + compaction
     evicted = 0
@@ -791,12 +843,14 @@ def prefill_evict(args, torch, emelk, dev):
     assert ok, err
     mv = torch.tensor(moves, dtype=torch.int32, device=dev)
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    emelk.copy_blocks(g, k_pool, v_pool, mv)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    copy_ms = e0.elapsed_time(e1)
+    # one untimed launch, then repeats of the same move list, each between
+    # its own HIP event pair after a GPU head start (the pools' contents are
+    # not used after this point)
+    copy_reps = 5
+    copy_times = timed_blocks(torch, stream, lambda: emelk.copy_blocks(g, k_pool, v_pool, mv),
+                              copy_reps,
+                              prime=lambda: emelk.copy_blocks(g, k_pool, v_pool, mv))
+    copy_ms = float(np.mean(copy_times))
     copy_bytes = 2 * 2 * len(moves) * L * page_bytes  # read + write, K and V
     traffic = PMC_TRAFFIC_BYTES.get(args.config)
     res = {
@@ -814,12 +868,16 @@ def prefill_evict(args, torch, emelk, dev):
                                         "--pmc FETCH_SIZE / WRITE_SIZE of an earlier run of this "
                                         "workload, copy-calibrated)") if traffic else None,
                      "algorithmic_bytes": prefill_bytes,
-                     "kernel": "prefill_kernel (HIP events per layer call)",
+                     "kernel": "prefill_kernel",
+                     "timing": "HIP events around K replays of a graph of the L chunk-attention "
+                               "calls, per call",
                      "flops_per_launch": flops_layer, "avg_launch_ms": round(attn_ms, 4)},
-        "kernel_split": split,
         "cpu_baseline": cpu,
         "parity_sample": parity,
         "compaction": {"pages_evicted": evicted, "moves": len(moves), "ms": round(copy_ms, 4),
+                       "timing": f"mean of {len(copy_times)} event-timed launches after an "
+                                 "untimed one (min "
+                                 f"{min(copy_times):.4f} ms, max {max(copy_times):.4f} ms)",
                        "GB/s": round(copy_bytes / (copy_ms * 1e-3) / 1e9, 1),
                        "bytes": copy_bytes,
                        "roofline": {"bound": "hbm", "kernel": "copy_blocks_kernel (HIP events)",

@@ -17,7 +17,7 @@
 //   MFMA route (head_dim <= 256, G <= 4, pages holding whole wave tiles):
 //   each 4-lane block of a wave holds 4 tokens of one 16-dim chunk; scores
 //   S^T = K . Q^T and the output O^T += V^T . P^T run on 4x4x4 MFMA blocks
-//   (fp16, or for q8_0 pools integer scores with q as 16-bit fixed point),
+//   (fp16 operands; q8_0 bytes as exact fp16 values),
 //   and each lane keeps one head's softmax and 16 output dims.
 //   Scalar route (other shapes): a lane holds 16 dims of two tokens, scores
 //   and P.V by v_dot2_f32_f16, a DPP sum over the row's lanes.
@@ -29,9 +29,9 @@
 //   actual lengths.
 //
 // q8_0 pools keep their int8 values exact: biased fp16 (b + 1152) for the
-// fp16 operands with the bias removed through the sums of the weights, and
-// the block scales applied to the scores and folded into the fp16 weights
-// p * d_v.
+// fp16 operands with the bias removed through the sums of q and of the
+// weights; the block scales are applied to the scores and folded into the
+// weights p * d_v, which enter the MFMA as an fp16 hi + lo pair.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -60,7 +60,9 @@ constexpr int k_decode_nb = 2;
 // shuffles that sum the blocks and hand P to the V lanes lengthened each
 // tile's dependent chain; the 4x4x4 block layout (scores and P.V both on
 // MFMA, no hand-over) is what made it faster.  Scaling K to fp16 before the
-// MFMA breaks the 2e-3 bar on the x20-outlier data.  Workgroups of 4 KV
+// MFMA breaks the 2e-3 bar on the x20-outlier data, and so does rounding
+// the P.V weights p * d_v once to fp16 on some shapes (the reference's own
+// fp16 rounding of P already spends half the bar there).  Workgroups of 4 KV
 // heads instead of 8 ran at 4.44 vs 5.51 TB/s there, and with 3 waves per
 // SIMD (168 VGPRs, one tile set in flight) at 3.06.
 
@@ -179,6 +181,15 @@ __device__ __forceinline__ void i8x16_pair_to_half2(const uint4_t w0, const uint
     out[4 * i + 2] = as_half2(__builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u));
     out[4 * i + 3] = as_half2(__builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u));
   }
+}
+
+// (x0, x1) as fp16 pairs hi + lo: hi = fp16(x), lo = fp16(x - hi), so hi + lo
+// carries x to about 2^-22 relative (|x| in the fp16 normal range; below it
+// to the fp16 subnormal step).  The q8_0 P.V weights p * d_v go to the MFMA
+// as both halves, so the output sees them at nearly fp32 accuracy.
+__device__ __forceinline__ void split_half2(float x0, float x1, half2_t &hi, half2_t &lo) {
+  hi = pack_half2(x0, x1);
+  lo = pack_half2(x0 - static_cast<float>(hi.x), x1 - static_cast<float>(hi.y));
 }
 
 template <int D, bool Q8>
@@ -315,14 +326,11 @@ struct decode_state {
   float acc[G][16];
   float kbias[G];    // q8_0: -1152 * sum of the lane's 16 q values (K byte bias)
   float vw[G];       // q8_0: sum of the fp16 P.V weights (V byte bias 1152 removed at the end)
-  // q8_0 scores on MFMA: q of head 4*g + lane%4 over the lane's 16 dims as
-  // 16-bit fixed point Q = 256 * hi + lo (q ~ Q * sq), hi and lo as int8
-  // operands in four 4-dim steps; sq per head of the lane's 16 dims
-  int qi[(G + 3) / 4][2][4];
-  float sq[G];
-  // f16 scores on MFMA: fp16 q of head lane%4 over the lane's 16 dims, in
-  // four 4-dim steps (the K row's order)
+  // scores on MFMA: fp16 q of head 4 * set + lane % 4 over the lane's 16
+  // dims, in four 4-dim steps (the K row's order), zero past G
   half4_t qm[(G + 3) / 4][4];
+  // q8_0 MPV route: the K byte bias of the lane's own head of each set
+  float kb[(G + 3) / 4];
 };
 
 template <int D, bool Q8>
@@ -338,31 +346,36 @@ __device__ __forceinline__ void consume_tile(decode_state<D, G, Q8> &S, const ti
   constexpr int LPT = D / 16;
   float y0[G], y1[G];
   if constexpr (MQK) {
-    // q8_0 scores on v_mfma_i32_4x4x4i8: each 4-lane block holds 4 tokens
-    // (B columns, the raw K bytes) of one 16-dim chunk and the q of 4 heads
-    // (A rows); lane 4b+j receives the 4 heads' sums for its token j over
-    // the chunk, exact in int32 (hi and lo of q separately).
-    static_assert(Q8, "integer scores need q8_0 keys");
-    const uint32_t kw0[4] = {T.k0.a.x, T.k0.a.y, T.k0.a.z, T.k0.a.w};
-    const uint32_t kw1[4] = {T.k1.a.x, T.k1.a.y, T.k1.a.z, T.k1.a.w};
+    // q8_0 scores on v_mfma_f32_4x4x4_16b_f16: each 4-lane block holds 4
+    // tokens (B columns: the K bytes as exact fp16 b + 1152) of one 16-dim
+    // chunk and the exact fp16 q of 4 heads (A rows); lane 4b+j receives the
+    // 4 heads' sums for its token j over the chunk.  Each accumulator starts
+    // at the head's -1152 * sum q, which removes the byte bias.
+    static_assert(Q8, "MFMA scores on this route need q8_0 keys");
+    half2_t kh0[8], kh1[8];
+    i8x16_to_half_biased(T.k0.a, kh0);
+    i8x16_to_half_biased(T.k1.a, kh1);
     const float ks0 = f16_bits_to_f32(static_cast<uint16_t>(T.k0.d)) * c;
     const float ks1 = f16_bits_to_f32(static_cast<uint16_t>(T.k1.d)) * c;
 #pragma unroll
     for (int g4 = 0; g4 < (G + 3) / 4; ++g4) {
-      int4_t h0 = {0, 0, 0, 0}, l0 = h0, h1 = h0, l1 = h0;
+      float4_t a0;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) a0[r] = 4 * g4 + r < G ? S.kbias[4 * g4 + r < G ? 4 * g4 + r : 0] : 0.0f;
+      float4_t a1 = a0;
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
-        h0 = __builtin_amdgcn_mfma_i32_4x4x4i8(S.qi[g4][0][m], static_cast<int>(kw0[m]), h0, 0, 0, 0);
-        h1 = __builtin_amdgcn_mfma_i32_4x4x4i8(S.qi[g4][0][m], static_cast<int>(kw1[m]), h1, 0, 0, 0);
-        l0 = __builtin_amdgcn_mfma_i32_4x4x4i8(S.qi[g4][1][m], static_cast<int>(kw0[m]), l0, 0, 0, 0);
-        l1 = __builtin_amdgcn_mfma_i32_4x4x4i8(S.qi[g4][1][m], static_cast<int>(kw1[m]), l1, 0, 0, 0);
+        const half4_t k0 = {kh0[2 * m].x, kh0[2 * m].y, kh0[2 * m + 1].x, kh0[2 * m + 1].y};
+        const half4_t k1 = {kh1[2 * m].x, kh1[2 * m].y, kh1[2 * m + 1].x, kh1[2 * m + 1].y};
+        a0 = __builtin_amdgcn_mfma_f32_4x4x4f16(S.qm[g4][m], k0, a0, 0, 0, 0);
+        a1 = __builtin_amdgcn_mfma_f32_4x4x4f16(S.qm[g4][m], k1, a1, 0, 0, 0);
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int h = 4 * g4 + r;
         if (h < G) {
-          y0[h] = chunk_sum<LPT>(static_cast<float>(h0[r] * 256 + l0[r]) * (S.sq[h] * ks0));
-          y1[h] = chunk_sum<LPT>(static_cast<float>(h1[r] * 256 + l1[r]) * (S.sq[h] * ks1));
+          y0[h] = chunk_sum<LPT>(a0[r] * ks0);
+          y1[h] = chunk_sum<LPT>(a1[r] * ks1);
           if constexpr (MASKED) {
             y0[h] = ok0 ? y0[h] : -INFINITY;
             y1[h] = ok1 ? y1[h] : -INFINITY;
@@ -457,13 +470,12 @@ __device__ __forceinline__ void consume_tile(decode_state<D, G, Q8> &S, const ti
     }
     S.l[h] += p0 + p1;
     if constexpr (Q8) {
-      // fp16 weights p * d_v (the f16 route rounds p to fp16 the same way);
-      // measured 5.14 TB/s against 4.85 for fp32 FMAs of p * d_v with the
-      // bytes converted to fp32, at the Llama-3-8B q8_0 shape
-      const half2_t ww = pack_half2(p0 * vs0, p1 * vs1);
+      // weights p * d_v as fp16 hi + lo pairs against the exact fp16 values
+      half2_t wh, wl;
+      split_half2(p0 * vs0, p1 * vs1, wh, wl);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) S.acc[h][i] = dot2(ww, vq[i], S.acc[h][i]);
-      S.vw[h] = dot2(ww, as_half2(0x3C003C00u), S.vw[h]);  // + w0 + w1
+      for (int i = 0; i < 16; ++i) S.acc[h][i] = dot2(wl, vq[i], dot2(wh, vq[i], S.acc[h][i]));
+      S.vw[h] = dot2(wl, as_half2(0x3C003C00u), dot2(wh, as_half2(0x3C003C00u), S.vw[h]));
     } else {
       const half2_t pp = pack_half2(p0, p1);
 #pragma unroll
@@ -485,13 +497,14 @@ __device__ __forceinline__ void consume_tile(decode_state<D, G, Q8> &S, const ti
 // one head.  T.k{0,1} hold the lane's own token row (token j + 4q of each
 // half); T.v{0,1} hold 4 dims of the chunk (mpv_dim) for the block's 4
 // tokens.
-//   q8_0: K bytes on v_mfma_i32_4x4x4_16b_i8 against q as 16-bit fixed
-//   point (hi and lo int8, exact int32 sums), scaled by the token's K block
-//   scale (from the lane that loaded it) and the lane's q scale; V.d is the
-//   lane's own token's V block scale, P' = p * d_v of each token (the lane's
-//   16 dims lie in one scale block), and the V bytes enter as the exact fp16
-//   values b + 1152 (the 1152 * sum P' term is removed at the end through
-//   vw).
+//   q8_0: K bytes as exact fp16 values b + 1152 on v_mfma_f32_4x4x4_16b_f16
+//   against the fp16 q (each accumulator starts at the lane's head's -1152 *
+//   sum q, which removes the bias), scaled by the token's K block scale
+//   (from the lane that loaded it); V.d is the lane's own token's V block
+//   scale, P' = p * d_v of each token (the lane's 16 dims lie in one scale
+//   block) as an fp16 hi + lo pair (two MFMAs), and the V bytes enter as
+//   the exact fp16 values b + 1152 (the 1152 * sum P' term is removed at the
+//   end through vw).
 //   f16: K halves on v_mfma_f32_4x4x4_16b_f16 against q in fp16; P' = p;
 //   V.a holds tokens 0 and 1 (two words each), V.b tokens 2 and 3.
 // ok0/ok1: the lane's own token is valid.
@@ -523,31 +536,32 @@ __device__ __forceinline__ void consume_tile_mpv(decode_state<D, G, Q8> &S,
       dk_b[hf][2] = quad_bcast<2>(dk);
       dk_b[hf][3] = quad_bcast<3>(dk);
     }
+    // K operand of step m (dims 4m .. 4m + 3 of the chunk), fp16; q8_0 bytes
+    // as exact fp16 b + 1152, the bias removed by the accumulator's start
+    half4_t ka[4];
+    if constexpr (Q8) {
+      half2_t kh[8];
+      i8x16_to_half_biased(K.a, kh);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) ka[m] = half4_t{kh[2 * m].x, kh[2 * m].y, kh[2 * m + 1].x, kh[2 * m + 1].y};
+    } else {
+      const uint32_t kw[8] = {K.a.x, K.a.y, K.a.z, K.a.w, K.b.x, K.b.y, K.b.z, K.b.w};
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const half2_t k01 = as_half2(kw[2 * m]), k23 = as_half2(kw[2 * m + 1]);
+        ka[m] = half4_t{k01.x, k01.y, k23.x, k23.y};
+      }
+    }
 #pragma unroll
     for (int hs = 0; hs < NHS; ++hs) {
-      if constexpr (Q8) {
-        const uint32_t kw[4] = {K.a.x, K.a.y, K.a.z, K.a.w};
-        int4_t hi = {0, 0, 0, 0}, lo = hi;
+      const float s0 = Q8 ? S.kb[hs] : 0.0f;
+      float4_t sc = {s0, s0, s0, s0};
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          hi = __builtin_amdgcn_mfma_i32_4x4x4i8(static_cast<int>(kw[m]), S.qi[hs][0][m], hi, 0, 0, 0);
-          lo = __builtin_amdgcn_mfma_i32_4x4x4i8(static_cast<int>(kw[m]), S.qi[hs][1][m], lo, 0, 0, 0);
-        }
-        // q's scale is this lane's head's (S.sq[hs])
+      for (int m = 0; m < 4; ++m) sc = __builtin_amdgcn_mfma_f32_4x4x4f16(ka[m], S.qm[hs][m], sc, 0, 0, 0);
+      if constexpr (Q8) {  // token i's K block scale (softmax scale folded in)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          y[hs][hf][i] =
-              chunk_sum<LPT>(static_cast<float>(hi[i] * 256 + lo[i]) * (dk_b[hf][i] * S.sq[hs]));
-        }
+        for (int i = 0; i < 4; ++i) y[hs][hf][i] = chunk_sum<LPT>(sc[i] * dk_b[hf][i]);
       } else {
-        const uint32_t kw[8] = {K.a.x, K.a.y, K.a.z, K.a.w, K.b.x, K.b.y, K.b.z, K.b.w};
-        float4_t sc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          const half2_t k01 = as_half2(kw[2 * m]), k23 = as_half2(kw[2 * m + 1]);
-          const half4_t ka = {k01.x, k01.y, k23.x, k23.y};
-          sc = __builtin_amdgcn_mfma_f32_4x4x4f16(ka, S.qm[hs][m], sc, 0, 0, 0);
-        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) y[hs][hf][i] = chunk_sum<LPT>(sc[i]) * c;
       }
@@ -637,12 +651,15 @@ __device__ __forceinline__ void consume_tile_mpv(decode_state<D, G, Q8> &S,
       }
       S.l[hs] += (p[0] + p[1]) + (p[2] + p[3]);
       half4_t pw;
-      if constexpr (Q8) {
-        const half2_t w01 = pack_half2(p[0] * dv_b[0], p[1] * dv_b[1]);
-        const half2_t w23 = pack_half2(p[2] * dv_b[2], p[3] * dv_b[3]);
-        S.vw[hs] = dot2(w01, as_half2(0x3C003C00u), S.vw[hs]);
-        S.vw[hs] = dot2(w23, as_half2(0x3C003C00u), S.vw[hs]);
-        pw = half4_t{w01.x, w01.y, w23.x, w23.y};
+      [[maybe_unused]] half4_t pl;
+      if constexpr (Q8) {  // P' = p * d_v as fp16 hi (pw) + lo (pl)
+        half2_t h01, l01, h23, l23;
+        split_half2(p[0] * dv_b[0], p[1] * dv_b[1], h01, l01);
+        split_half2(p[2] * dv_b[2], p[3] * dv_b[3], h23, l23);
+        const half2_t one = as_half2(0x3C003C00u);
+        S.vw[hs] = dot2(l23, one, dot2(h23, one, dot2(l01, one, dot2(h01, one, S.vw[hs]))));
+        pw = half4_t{h01.x, h01.y, h23.x, h23.y};
+        pl = half4_t{l01.x, l01.y, l23.x, l23.y};
       } else {
         const half2_t w01 = pack_half2(p[0], p[1]);
         const half2_t w23 = pack_half2(p[2], p[3]);
@@ -653,6 +670,7 @@ __device__ __forceinline__ void consume_tile_mpv(decode_state<D, G, Q8> &S,
         float4_t o = {S.acc[hs][4 * sd], S.acc[hs][4 * sd + 1], S.acc[hs][4 * sd + 2],
                       S.acc[hs][4 * sd + 3]};
         o = __builtin_amdgcn_mfma_f32_4x4x4f16(va[sd], pw, o, 0, 0, 0);
+        if constexpr (Q8) o = __builtin_amdgcn_mfma_f32_4x4x4f16(va[sd], pl, o, 0, 0, 0);
         S.acc[hs][4 * sd] = o.x;
         S.acc[hs][4 * sd + 1] = o.y;
         S.acc[hs][4 * sd + 2] = o.z;
@@ -683,7 +701,7 @@ __device__ __forceinline__ void consume_any(decode_state<D, G, Q8> &S, const til
 // every row of a (tile, half) lies in one page: the page id is moved to a
 // scalar register once per half-tile and each lane adds a fixed offset.
 //
-// MQK (q8_0, head_dim <= 256): scores on integer MFMA.  The lane layout
+// MQK (q8_0, head_dim <= 256): scores on 4x4x4 MFMA.  The lane layout
 // then puts the 4 tokens of an MFMA block in lane bits 0-1 and the 16-dim
 // chunk in the bits above them: lane = j + 4 * chunk + 4 * LPT * q holds
 // chunk `chunk` of token j + 4 * q of each half-tile.
@@ -735,8 +753,12 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
     slot_base = static_cast<uint64_t>(w) * P.L.n_head + kvh * G;
     slot_stride = 1u;
   } else {
-    len = P.row_q_start != nullptr ? P.row_q_start[seq / P.rows] + (seq % P.rows) + 1
-                                   : P.kv_lens[seq];
+    if (P.row_q_start != nullptr) {  // a negative chunk start attends to nothing (zero rows)
+      const int32_t q0 = P.row_q_start[seq / P.rows];
+      len = q0 < 0 ? 0 : q0 + (seq % P.rows) + 1;
+    } else {
+      len = P.kv_lens[seq];
+    }
     slot_base = (static_cast<uint64_t>(seq) * P.L.n_head + kvh * G) * P.max_splits + split;
     slot_stride = static_cast<uint32_t>(P.max_splits);
   }
@@ -820,7 +842,7 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
       qsum += static_cast<float>(S.qh[h][j].x) + static_cast<float>(S.qh[h][j].y);
     }
     S.kbias[h] = -1152.0f * qsum;
-    if constexpr (MQK && !Q8) {  // B operand of head set h / 4: head h % 4 == lane % 4 (zero past G)
+    if constexpr (MQK) {  // MFMA operand of head set h / 4: head h % 4 == lane % 4 (zero past G)
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
         if (h % 4 == 0) S.qm[h / 4][m] = half4_t{0, 0, 0, 0};
@@ -829,56 +851,14 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
                                    S.qh[h][2 * m + 1].y};
         }
       }
-    }
-    if constexpr (MQK && Q8) {
-      float mx = 0.0f;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        mx = fmaxf(mx, fmaxf(fabsf(static_cast<float>(S.qh[h][j].x)),
-                             fabsf(static_cast<float>(S.qh[h][j].y))));
-      }
-      // |Q| <= 32639 keeps hi = (Q + 128) >> 8 inside int8
-      S.sq[h] = mx / 32639.0f;
-      const float inv = mx > 0.0f ? 32639.0f / mx : 0.0f;
-      uint32_t hw[4] = {0u, 0u, 0u, 0u}, lw[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const half2_t pr = S.qh[h][i / 2];
-        const float qv = static_cast<float>(i % 2 == 0 ? pr.x : pr.y);
-        const int32_t Q = static_cast<int32_t>(__builtin_rintf(qv * inv));
-        const int32_t hi = (Q + 128) >> 8;
-        const int32_t lo = Q - hi * 256;
-        hw[i / 4] |= (static_cast<uint32_t>(hi) & 0xFFu) << (8 * (i % 4));
-        lw[i / 4] |= (static_cast<uint32_t>(lo) & 0xFFu) << (8 * (i % 4));
-      }
-      // A-operand row of this lane: head 4 * g + lane % 4 (zero past G)
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        if (h % 4 == 0) S.qi[h / 4][0][m] = S.qi[h / 4][1][m] = 0;
-        if (h % 4 == (lane & 3)) {
-          S.qi[h / 4][0][m] = static_cast<int>(hw[m]);
-          S.qi[h / 4][1][m] = static_cast<int>(lw[m]);
-        }
-      }
+      if (h % 4 == 0) S.kb[h / 4] = 0.0f;
+      if (h % 4 == (lane & 3)) S.kb[h / 4] = S.kbias[h];
     }
     S.m[h] = -INFINITY;
     S.l[h] = 0.0f;
     if constexpr (Q8) S.vw[h] = 0.0f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) S.acc[h][i] = 0.0f;
-  }
-
-  if constexpr (MPV && Q8) {  // the scales of the lane's B-operand heads, head set hs in sq[hs]
-    constexpr int NHS = (G + 3) / 4;
-    float sqo[NHS];
-#pragma unroll
-    for (int hs = 0; hs < NHS; ++hs) {
-      sqo[hs] = 0.0f;
-#pragma unroll
-      for (int h = 4 * hs; h < 4 * hs + 4 && h < G; ++h) sqo[hs] = h % 4 == (lane & 3) ? S.sq[h] : sqo[hs];
-    }
-#pragma unroll
-    for (int hs = 0; hs < NHS; ++hs) S.sq[hs] = sqo[hs];
   }
 
   const uint8_t *k_base = P.k_pool + static_cast<uint64_t>(P.layer) * P.L.layer_bytes +
@@ -1354,11 +1334,9 @@ int32_t device_cu_count() {
   return cus;
 }
 
-// A balanced plan (every wave derives splits of equal size over all tokens
-// of a ragged batch from kv_lens) measured no faster on MI355X: 33.5 vs
-// 33.1 us for 16 sequences of 1k-4k tokens at Llama-3.2-1B, because the
-// extra round trip for every length adds about 3 us of start-up while the
-// marginal streaming rate (6.3 TB/s past ~1k tokens) is already reached.
+// This is the host plan: the fixed split size, and the bound on the
+// balanced plan the kernels derive on the device for 2 to 64 sequences
+// (balanced_splits).
 //
 // Split sizing: about one workgroup per CU (a workgroup is 8 waves, which is
 // what one CU holds at this kernel's register budget; more, shorter splits
@@ -1683,12 +1661,25 @@ static __device__ __align__(256) uint8_t scratch[EMELK_DECODE_STATIC_SCRATCH_BYT
 constexpr int k_max_devices = 64;
 std::atomic<void *> scratch_ptr[k_max_devices];
 
-// This device's copy of `scratch` (nullptr with *err set on failure).
-void *device_scratch(emel_error_type *err) {
+// The copy of `scratch` on the device of `stream`, which must be the current
+// device (the symbol lookup resolves on the current device); nullptr with
+// *err set otherwise.  A null stream is the current device's.
+void *device_scratch(void *stream, emel_error_type *err) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= k_max_devices) {
     *err = EMELK_ERR_BACKEND;
     return nullptr;
+  }
+  if (stream != nullptr) {
+    hipDevice_t sdev = -1;
+    if (hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev) != hipSuccess) {
+      *err = EMELK_ERR_BACKEND;
+      return nullptr;
+    }
+    if (sdev != dev) {  // another GPU's stream: its kernels must not get this GPU's array
+      *err = EMELK_ERR_INVALID_REQUEST;
+      return nullptr;
+    }
   }
   void *p = scratch_ptr[dev].load(std::memory_order_acquire);
   if (p == nullptr) {
@@ -1725,7 +1716,7 @@ extern "C" emel_error_type emelk_attn_decode_noalloc(
     return EMELK_ERR_INVALID_REQUEST;
   }
   emel_error_type err = EMELK_ERR_NONE;
-  void *ws = device_scratch(&err);
+  void *ws = device_scratch(stream, &err);
   if (ws == nullptr) return err;
   return decode_impl(g, k_pool, v_pool, layer, q, out, n_seq, kv_lens, max_kv_len, block_tables,
                      table_stride, scale, ws, EMELK_DECODE_STATIC_SCRATCH_BYTES, stream, k_rows,

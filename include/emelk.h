@@ -321,7 +321,8 @@ emel_error_type emelk_attn_decode_contiguous(const emelk_kv_geometry *g, void *k
  * (emelk_attn_decode_plan's bytes_out) exceeds that size returns
  * EMELK_ERR_OUT_OF_MEMORY before touching the device.  Every call on one
  * GPU uses that GPU's one array: calls that overlap on one GPU (other
- * streams, other threads) race. */
+ * streams, other threads) race.  The stream must belong to the current
+ * device (a stream of another device returns EMELK_ERR_INVALID_REQUEST). */
 #define EMELK_DECODE_STATIC_SCRATCH_BYTES (16u << 20)
 emel_error_type emelk_attn_decode_noalloc(const emelk_kv_geometry *g, void *k_pool, void *v_pool,
                                           int32_t layer, const float *k_rows, const float *v_rows,
@@ -334,7 +335,9 @@ emel_error_type emelk_attn_decode_noalloc(const emelk_kv_geometry *g, void *k_po
  * [n_seq][n_q][n_head][head_dim]; row r of sequence s attends causally to
  * logical positions [0, q_start[s] + r] (the chunk must already be appended).
  * Replaces the per-row store + attend loop of run_prefill
- * (text/generator/detail.hpp:4297-4372).  head_dim 64 and 128 run on MFMA,
+ * (text/generator/detail.hpp:4297-4372).  A negative q_start[s] makes every
+ * row of sequence s attend to nothing: its rows are written as zeros, on
+ * every route.  head_dim 64 and 128 run on MFMA,
  * f16 and q8_0 pools alike (q8_0 K values enter the score MFMAs exactly, as
  * two fp16 parts, values of magnitude 65520 or more excepted; q8_0 V values
  * as fp16(q * d), one rounding), and so do

@@ -24,8 +24,7 @@ _u16p = ctypes.POINTER(ctypes.c_uint16)
 _i32p = ctypes.POINTER(ctypes.c_int32)
 _vp = ctypes.c_void_p
 
-lib = ctypes.CDLL(LIB_PATH)
-for name, res, args in [
+_SIGNATURES = [
     ("orc_fp32_to_fp16", ctypes.c_uint16, [ctypes.c_float]),
     ("orc_fp16_to_fp32", ctypes.c_float, [ctypes.c_uint16]),
     ("orc_fp32_to_fp16_sweep", ctypes.c_uint64, [ctypes.c_uint64, ctypes.c_uint64]),
@@ -60,10 +59,43 @@ for name, res, args in [
      [_f32p, _u16p, _u16p, _u16p, ctypes.c_int32, _i32p, ctypes.c_int32, ctypes.c_int32,
       ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_float, _f32p,
       ctypes.c_int32]),
-]:
-    fn = getattr(lib, name)
-    fn.restype = res
-    fn.argtypes = args
+    ("orc_attention_rows", ctypes.c_double,
+     [ctypes.c_int32, _f32p, _vp, _vp, _u16p, ctypes.c_int32, _i32p, _i32p, ctypes.c_int32,
+      ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+      ctypes.c_float, _f32p, ctypes.c_int32]),
+]
+
+
+def _load(path):
+    lib_ = ctypes.CDLL(path)
+    for name, res, args in _SIGNATURES:
+        fn = getattr(lib_, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib_
+
+
+lib = _load(LIB_PATH)
+_native = None
+
+
+def native_lib():
+    """The oracle built -O3 -march=native on this host (the CPU baseline's
+    build), compiled on first use by `make native`; (lib, build note).
+    Falls back to the portable build, saying so, when the compiler fails."""
+    global _native
+    if _native is None:
+        import subprocess
+        try:
+            subprocess.run(["make", "-s", "-C", _HERE, "native"], check=True,
+                           capture_output=True, timeout=120)
+            _native = (_load(os.path.join(_HERE, "_native", "liboracle.so")),
+                       "gcc -O3 -march=native -ffp-contract=off, built on this host")
+        except Exception as e:  # noqa: BLE001 - reported on the baseline line
+            _native = (lib, f"portable -O3 build (native build failed: {e!r})")
+    return _native
+
+
 
 
 def _p(a, t):
@@ -134,10 +166,11 @@ def compute_attention_q8_0(q, key_cache, value_cache, blocks, block_tokens, n_he
 
 
 def flash_attn_f16acc(q, k_headmajor, v_headmajor, head_dim, n_head, n_head_kv, kv_tokens,
-                      kv_stride_tokens, scale):
+                      kv_stride_tokens, scale, lib_=None):
+    lib_ = lib if lib_ is None else lib_
     q = np.ascontiguousarray(q, dtype=np.float32)
     out = np.zeros(n_head * head_dim, dtype=np.float32)
-    ok = lib.orc_flash_attn_f16acc(_p(q, _f32p), _p(k_headmajor, _u16p), _p(v_headmajor, _u16p),
+    ok = lib_.orc_flash_attn_f16acc(_p(q, _f32p), _p(k_headmajor, _u16p), _p(v_headmajor, _u16p),
                                    head_dim, n_head, n_head_kv, kv_tokens, kv_stride_tokens,
                                    scale, _p(out, _f32p))
     if not ok:
@@ -157,17 +190,39 @@ def attention_f64(q, k, v, n_head, n_head_kv, head_dim, kv_tokens, inv_scale):
 
 
 def decode_batch_f16(q, key_cache, value_cache, block_tables, position_limits, block_tokens,
-                     n_head, n_head_kv, head_dim, n_ctx, inv_scale, n_threads):
+                     n_head, n_head_kv, head_dim, n_ctx, inv_scale, n_threads, lib_=None):
     """Threaded reference route over a batch; returns (out, seconds)."""
     q = np.ascontiguousarray(q, dtype=np.float32)
     block_tables = np.ascontiguousarray(block_tables, dtype=np.uint16)
     limits = np.ascontiguousarray(position_limits, dtype=np.int32)
     n_seq = q.shape[0]
     out = np.zeros((n_seq, n_head * head_dim), dtype=np.float32)
-    secs = lib.orc_decode_batch_f16(_p(q, _f32p), _p(key_cache, _u16p), _p(value_cache, _u16p),
+    lib_ = lib if lib_ is None else lib_
+    secs = lib_.orc_decode_batch_f16(_p(q, _f32p), _p(key_cache, _u16p), _p(value_cache, _u16p),
                                     _p(block_tables, _u16p), block_tables.shape[1],
                                     _p(limits, _i32p), n_seq, block_tokens, n_head, n_head_kv,
                                     head_dim, n_ctx, inv_scale, _p(out, _f32p), n_threads)
+    return out, float(secs)
+
+
+def attention_rows(kind, q, key_cache, value_cache, block_tables, limits, block_tokens, n_head,
+                   n_head_kv, head_dim, inv_scale, n_threads, row_table=None, n_ctx=0,
+                   lib_=None):
+    """Threaded reference route over rows (orc_attention_rows): kind "f16" or
+    "q8_0"; row i uses table row row_table[i] (i when None) and attends to
+    [0, limits[i]).  Returns (out [n_rows, n_head*head_dim], seconds)."""
+    lib_ = lib if lib_ is None else lib_
+    q = np.ascontiguousarray(q, dtype=np.float32).reshape(len(limits), -1)
+    block_tables = np.ascontiguousarray(block_tables, dtype=np.uint16)
+    limits = np.ascontiguousarray(limits, dtype=np.int32)
+    rt = None if row_table is None else np.ascontiguousarray(row_table, dtype=np.int32)
+    out = np.zeros((len(limits), n_head * head_dim), dtype=np.float32)
+    secs = lib_.orc_attention_rows(0 if kind == "f16" else 1, _p(q, _f32p),
+                                   key_cache.ctypes.data_as(_vp), value_cache.ctypes.data_as(_vp),
+                                   _p(block_tables, _u16p), block_tables.shape[1],
+                                   None if rt is None else _p(rt, _i32p), _p(limits, _i32p),
+                                   len(limits), block_tokens, n_head, n_head_kv, head_dim, n_ctx,
+                                   inv_scale, _p(out, _f32p), n_threads)
     return out, float(secs)
 
 

@@ -421,51 +421,85 @@ void orc_attention_f64(const float *q, const float *k, const float *v, int32_t n
 
 /* ---- batched CPU baseline driver (one thread per sequence lane) ---------- */
 
+/* Rows of attention over paged caches, spread over threads: row i uses
+ * block-table row row_table[i] (identity when NULL) and attends to
+ * [0, limits[i]); its softmax spans n_ctx positions (limits[i] when n_ctx
+ * <= 0).  kind 0: f16 caches (orc_compute_attention_f16), 1: q8_0
+ * (orc_compute_attention_q8_0).  Threads take rows in order from a shared
+ * counter, so long and short rows balance.  Returns the wall seconds of
+ * the compute alone. */
 typedef struct {
+  int32_t kind;
   const float *q;
-  const uint16_t *key_cache, *value_cache, *block_tables;
-  const int32_t *position_limits;
-  int32_t table_stride, n_seq, bt, n_head, n_head_kv, head_dim, n_ctx, stride_threads, first;
+  const void *key_cache, *value_cache;
+  const uint16_t *block_tables;
+  const int32_t *row_table, *limits;
+  int32_t table_stride, n_rows, bt, n_head, n_head_kv, head_dim, n_ctx;
   float inv_scale;
   float *out;
-} orc_batch_job;
+  int32_t next; /* shared row counter */
+} orc_rows_job;
 
-static void *batch_worker(void *arg) {
-  const orc_batch_job *j = (const orc_batch_job *)arg;
-  float *scratch = (float *)malloc(sizeof(float) * 4 * (size_t)j->n_ctx);
+static void *rows_worker(void *arg) {
+  orc_rows_job *j = (orc_rows_job *)arg;
+  int32_t max_ctx = j->n_ctx;
+  for (int32_t i = 0; i < j->n_rows; ++i) max_ctx = j->limits[i] > max_ctx ? j->limits[i] : max_ctx;
+  float *scratch = (float *)malloc(sizeof(float) * 4 * (size_t)(max_ctx > 0 ? max_ctx : 1));
   const int64_t qd = (int64_t)j->n_head * j->head_dim;
-  for (int32_t s = j->first; s < j->n_seq; s += j->stride_threads) {
-    orc_compute_attention_f16(j->q + s * qd, j->key_cache, j->value_cache,
-                              j->block_tables + (int64_t)s * j->table_stride, j->bt, j->n_head,
-                              j->n_head_kv, j->head_dim, j->position_limits[s], j->n_ctx,
-                              j->inv_scale, j->out + s * qd, scratch);
+  for (;;) {
+    const int32_t i = __atomic_fetch_add(&j->next, 1, __ATOMIC_RELAXED);
+    if (i >= j->n_rows) break;
+    const int32_t t = j->row_table != NULL ? j->row_table[i] : i;
+    const int32_t lim = j->limits[i];
+    const int32_t n_ctx = j->n_ctx > 0 ? j->n_ctx : lim;
+    const uint16_t *blocks = j->block_tables + (int64_t)t * j->table_stride;
+    if (j->kind == 0) {
+      orc_compute_attention_f16(j->q + i * qd, (const uint16_t *)j->key_cache,
+                                (const uint16_t *)j->value_cache, blocks, j->bt, j->n_head,
+                                j->n_head_kv, j->head_dim, lim, n_ctx, j->inv_scale,
+                                j->out + i * qd, scratch);
+    } else {
+      orc_compute_attention_q8_0(j->q + i * qd, (const orc_block_q8_0 *)j->key_cache,
+                                 (const orc_block_q8_0 *)j->value_cache, blocks, j->bt, j->n_head,
+                                 j->n_head_kv, j->head_dim, lim, n_ctx, j->inv_scale,
+                                 j->out + i * qd, scratch);
+    }
   }
   free(scratch);
   return NULL;
 }
 
+double orc_attention_rows(int32_t kind, const float *q, const void *key_cache,
+                          const void *value_cache, const uint16_t *block_tables,
+                          int32_t table_stride, const int32_t *row_table,
+                          const int32_t *limits, int32_t n_rows, int32_t bt, int32_t n_head,
+                          int32_t n_head_kv, int32_t head_dim, int32_t n_ctx, float inv_scale,
+                          float *out, int32_t n_threads) {
+  if (n_threads < 1) n_threads = 1;
+  if (n_threads > n_rows) n_threads = n_rows > 0 ? n_rows : 1;
+  pthread_t *th = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)n_threads);
+  orc_rows_job job = {kind, q, key_cache, value_cache, block_tables, row_table, limits,
+                      table_stride, n_rows, bt, n_head, n_head_kv, head_dim, n_ctx, inv_scale,
+                      out, 0};
+  struct timespec t0, t1;
+  clock_gettime(CLOCK_MONOTONIC, &t0);
+  for (int32_t i = 0; i < n_threads; ++i) pthread_create(&th[i], NULL, rows_worker, &job);
+  for (int32_t i = 0; i < n_threads; ++i) pthread_join(th[i], NULL);
+  clock_gettime(CLOCK_MONOTONIC, &t1);
+  free(th);
+  return (double)(t1.tv_sec - t0.tv_sec) + 1e-9 * (double)(t1.tv_nsec - t0.tv_nsec);
+}
+
+/* The f16 batch of one decode step: sequence s uses table row s and
+ * attends to [0, position_limits[s]) with an n_ctx-wide softmax. */
 double orc_decode_batch_f16(const float *q, const uint16_t *key_cache, const uint16_t *value_cache,
                             const uint16_t *block_tables, int32_t table_stride,
                             const int32_t *position_limits, int32_t n_seq, int32_t bt,
                             int32_t n_head, int32_t n_head_kv, int32_t head_dim, int32_t n_ctx,
                             float inv_scale, float *out, int32_t n_threads) {
-  if (n_threads < 1) n_threads = 1;
-  if (n_threads > n_seq) n_threads = n_seq;
-  pthread_t *th = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)n_threads);
-  orc_batch_job *jobs = (orc_batch_job *)malloc(sizeof(orc_batch_job) * (size_t)n_threads);
-  struct timespec t0, t1;
-  clock_gettime(CLOCK_MONOTONIC, &t0);
-  for (int32_t i = 0; i < n_threads; ++i) {
-    jobs[i] = (orc_batch_job){q, key_cache, value_cache, block_tables, position_limits,
-                              table_stride, n_seq, bt, n_head, n_head_kv, head_dim, n_ctx,
-                              n_threads, i, inv_scale, out};
-    pthread_create(&th[i], NULL, batch_worker, &jobs[i]);
-  }
-  for (int32_t i = 0; i < n_threads; ++i) pthread_join(th[i], NULL);
-  clock_gettime(CLOCK_MONOTONIC, &t1);
-  free(th);
-  free(jobs);
-  return (double)(t1.tv_sec - t0.tv_sec) + 1e-9 * (double)(t1.tv_nsec - t0.tv_nsec);
+  return orc_attention_rows(0, q, key_cache, value_cache, block_tables, table_stride, NULL,
+                            position_limits, n_seq, bt, n_head, n_head_kv, head_dim, n_ctx,
+                            inv_scale, out, n_threads);
 }
 
 /* ---- the step before append --------------------------------------------- */

@@ -94,7 +94,7 @@ void orc_attention_f64(const float *q, const float *k, const float *v, int32_t n
 
 /*
  * Batched paged decode over a whole batch for one layer, the CPU baseline
- * driver: one std thread per sequence lane (up to n_threads).  Layout as
+ * driver: sequences spread over up to n_threads threads.  Layout as
  * orc_compute_attention_f16; block tables are [n_seq][table_stride].
  * position_limits[s] = tokens to attend for sequence s.  Returns wall seconds.
  */
@@ -104,6 +104,21 @@ double orc_decode_batch_f16(const float *q, const uint16_t *key_cache,
                             int32_t n_seq, int32_t block_tokens, int32_t n_head,
                             int32_t n_head_kv, int32_t head_dim, int32_t n_ctx,
                             float inv_scale, float *out, int32_t n_threads);
+
+/*
+ * Rows of attention for the CPU baseline, spread over up to n_threads
+ * threads (a shared row counter balances rows of different lengths).  Row i
+ * takes q row i, block-table row row_table[i] (row i when row_table is
+ * NULL) and attends to [0, limits[i]) with an n_ctx-wide softmax (limits[i]
+ * when n_ctx <= 0).  kind 0: f16 caches, 1: q8_0 caches (orc_block_q8_0
+ * rows).  Returns wall seconds.
+ */
+double orc_attention_rows(int32_t kind, const float *q, const void *key_cache,
+                          const void *value_cache, const uint16_t *block_tables,
+                          int32_t table_stride, const int32_t *row_table,
+                          const int32_t *limits, int32_t n_rows, int32_t block_tokens,
+                          int32_t n_head, int32_t n_head_kv, int32_t head_dim, int32_t n_ctx,
+                          float inv_scale, float *out, int32_t n_threads);
 
 #ifdef __cplusplus
 }

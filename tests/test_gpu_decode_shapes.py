@@ -1,10 +1,11 @@
-"""Seeded sweep of decode shapes against the oracle's reference route and the
-fp64 ideal (2e-3 abs + 1e-2 rel; q8_0 pools, which carry outliers, also
-allow the fp16 rounding of the probabilities): head_dim 64/128/256, 1-8 query heads per
+"""Seeded sweep of decode shapes against the oracle's reference route (2e-3
+abs + 1e-2 rel) and the fp64 ideal (the same bar; q8_0 pools, which carry
+outliers, also allow the reference's fp16 rounding of the probabilities
+there): head_dim 64/128/256, 1-8 query heads per
 KV head, 1-8 KV heads, page sizes that do and do not hold a whole wave tile,
 f16 and q8_0 pools, 1-70 ragged sequences, and pools whose never-written
 bytes are NaN patterns.  It covers the decode kernel's routes together: the
-MFMA route (scores and P.V on 4x4x4 blocks), the q8_0 integer-score route,
+MFMA route (scores and P.V on 4x4x4 blocks), the q8_0 MFMA-score route,
 the scalar route, the fixed and the balanced split plans, and one split per
 sequence."""
 import numpy as np
@@ -56,11 +57,12 @@ def test_decode_shape_sweep(device, case):
         assert_close(got, sc.oracle_decode(0, q), what="gpu vs reference route")
         assert_close(got, sc.ideal_decode(0, q), what="gpu vs fp64 ideal")
         return
-    # q8_0 pools carry x20 outliers.  Beyond the bar, both comparisons allow
-    # 2^-10 of sum_p p |v| per output: twice the 2^-11 bound of an fp16
-    # rounding of P, since the reference route rounds its own P too.  With
-    # outliers that sum dwarfs a cancelling output (the q8_0 prefill is held
-    # to the same allowance against the ideal).
+    # Against the reference route: the plain bar.  Against the fp64 ideal,
+    # q8_0 pools (x20 outliers) also allow 2^-10 of sum_p p |v| per output:
+    # the reference route's own fp16 rounding of P (2^-11 relative per
+    # weight) moves it that far from the ideal when outliers make sum_p p |v|
+    # much larger than a cancelling output.
+    assert_close(got, sc.oracle_decode(0, q), what="gpu vs reference route")
     scale = 1.0 / np.sqrt(D)
     qr = oracle.fp16_to_fp32(oracle.fp32_to_fp16(q))
     mag = np.zeros_like(got)
@@ -68,6 +70,5 @@ def test_decode_shape_sweep(device, case):
         k = oracle.dequantize_q8_0(oracle.quantize_q8_0(sc.k_rows[0][s_]))
         v = oracle.dequantize_q8_0(oracle.quantize_q8_0(sc.v_rows[0][s_]))
         mag[s_] = oracle.attention_f64(qr[s_], k, np.abs(v), sc.n_head, n_kv, D, n, scale)
-    atol = 2e-3 + 2.0 ** -10 * mag
-    assert_close(got, sc.oracle_decode(0, q), atol=atol, what="gpu vs reference route")
-    assert_close(got, sc.ideal_decode(0, q), atol=atol, what="gpu vs fp64 ideal")
+    assert_close(got, sc.ideal_decode(0, q), atol=2e-3 + 2.0 ** -10 * mag,
+                 what="gpu vs fp64 ideal")

@@ -545,6 +545,33 @@ def test_prefill_masks_invalid_pages_and_never_reads_unwritten_slots(device, n_h
     np.testing.assert_array_equal(got2[1], np.zeros_like(got2[1]))
 
 
+@pytest.mark.parametrize("kv_type,D", [("q8_0", 512), ("q8_0", 128), ("f16", 128)])
+def test_prefill_negative_q_start_writes_zero_rows_on_every_route(device, kv_type, D):
+    # q8_0 at head_dim 512 runs row by row through the decode kernel; the
+    # others on the MFMA prefill kernel.  Each route must treat a negative
+    # q_start as a sequence that attends to nothing: zero rows, and the other
+    # sequence's rows unchanged.
+    import torch
+    banner(f"prefill with a negative q_start, {kv_type} D={D}")
+    kt = emelk.KV_Q8_0 if kv_type == "q8_0" else emelk.KV_F16
+    n_q, q_starts = 12, [40, 20]
+    sc = Scenario(n_layer=1, n_head=4, n_kv=1, head_dim=D, block_tokens=16,
+                  lens=[q + n_q for q in q_starts], seed=46, kv_type=kt)
+    q = np.random.default_rng(47).standard_normal((2, n_q, 4, D)).astype(np.float32)
+    qd = torch.from_numpy(q).to(device)
+    outs = []
+    for starts in (q_starts, [q_starts[0], -3]):
+        out = torch.full_like(qd, float("nan"))
+        emelk.prefill_chunk(sc.g, sc.k_pool, sc.v_pool, 0, qd, out,
+                            torch.tensor(starts, dtype=torch.int32, device=device), sc.tables,
+                            1 / np.sqrt(D))
+        torch.cuda.synchronize()
+        outs.append(out.cpu().numpy())
+    assert np.isfinite(outs[0]).all()
+    np.testing.assert_array_equal(outs[1][0], outs[0][0])
+    np.testing.assert_array_equal(outs[1][1], np.zeros_like(outs[1][1]))
+
+
 def test_decode_masks_invalid_pages_and_short_tables(device):
     # Tokens on pages marked EMELK_INVALID_KV_BLOCK (0xFFFF), or past the end
     # of the table row, are left out of the softmax instead of being read

@@ -5,9 +5,9 @@ fp64 ideal, at the 2e-3 abs + 1e-2 rel bar.  It covers head_dim 64/128/256/
 512, 1-8 query heads per KV head, pages of 8-64 tokens (whole 32-key
 sub-tiles per page and not), f16 and q8_0 pools, empty and ragged prefixes,
 chunks of 1-100 rows, and NaN-filled pools with an invalid page in a
-prefix.  q8_0 pools carry x20 outliers and, beyond the bar, allow the fp16
-rounding of P and of the staged V: 2^-10 of sum_p p |v| per output (the
-reference route rounds its own P too)."""
+prefix.  Against the reference route every case is held to the plain bar;
+against the fp64 ideal, q8_0 pools (x20 outliers) also allow 2^-10 of
+sum_p p |v| per output, the reference route's own fp16 rounding of P."""
 import numpy as np
 import pytest
 
@@ -87,7 +87,7 @@ def test_prefill_shape_sweep(device, case):
             kk, vv, n = kf[:limit][keep], vf[:limit][keep], int(keep.sum())
             ideal = oracle.attention_f64(qr, kk, vv, n_head, n_kv, D, n, scale)
             atol = 2e-3
-            if q8:
+            if q8:  # the reference's own fp16 rounding of P, against the ideal only
                 mag = oracle.attention_f64(qr, kk, np.abs(vv), n_head, n_kv, D, n, scale)
                 atol = 2e-3 + 2.0 ** -10 * np.asarray(mag)
             g = got[s, r].ravel()
@@ -96,4 +96,4 @@ def test_prefill_shape_sweep(device, case):
                 fn = oracle.compute_attention_q8_0 if q8 else oracle.compute_attention_f16
                 want = fn(q[s, r].ravel(), kc, vc, sc.tables_host[s], bt, n_head, n_kv, D, limit,
                           limit, scale)
-                assert_close(g, want, atol=atol, what=f"seq {s} row {r} vs reference route")
+                assert_close(g, want, what=f"seq {s} row {r} vs reference route")

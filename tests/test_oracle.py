@@ -277,3 +277,37 @@ def test_decode_batch_threads_equal_per_sequence_route_bit_for_bit():
         assert secs >= 0.0
         assert got.shape == want.shape
         np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("kind", ["f16", "q8_0"])
+def test_attention_rows_equal_per_row_route_bit_for_bit(kind):
+    """orc_attention_rows (the bench's threaded CPU baseline for decode
+    batches and chunked-prefill rows) is the per-row route on worker
+    threads: any thread count, rows sharing a table row (a prefill chunk's
+    rows), and the -march=native build all give the per-row outputs bit for
+    bit."""
+    rng = np.random.default_rng(12)
+    n_head, n_kv, D, bt, n_blocks, stride = 8, 2, 64, 16, 64, 8
+    kv_dim = n_kv * D
+    rows_k = rng.standard_normal((n_blocks * bt, kv_dim)).astype(np.float32)
+    rows_v = rng.standard_normal((n_blocks * bt, kv_dim)).astype(np.float32)
+    if kind == "f16":
+        kc, vc = oracle.fp32_to_fp16(rows_k), oracle.fp32_to_fp16(rows_v)
+        route = oracle.compute_attention_f16
+    else:
+        kc, vc = oracle.quantize_q8_0(rows_k), oracle.quantize_q8_0(rows_v)
+        route = oracle.compute_attention_q8_0
+    tables = np.stack([rng.permutation(n_blocks)[:stride] for _ in range(3)]).astype(np.uint16)
+    n_rows = 9
+    row_table = np.array([0, 0, 0, 1, 1, 2, 2, 2, 2], np.int32)
+    limits = rng.integers(1, stride * bt + 1, size=n_rows).astype(np.int32)
+    q = rng.standard_normal((n_rows, n_head * D)).astype(np.float32)
+    scale = 1.0 / np.sqrt(D)
+    want = np.stack([route(q[i], kc, vc, tables[row_table[i]], bt, n_head, n_kv, D,
+                           int(limits[i]), int(limits[i]), scale) for i in range(n_rows)])
+    native, _note = oracle.native_lib()
+    for threads, lib_ in ((1, None), (4, None), (16, None), (5, native)):
+        got, secs = oracle.attention_rows(kind, q, kc, vc, tables, limits, bt, n_head, n_kv, D,
+                                          scale, threads, row_table=row_table, lib_=lib_)
+        assert secs >= 0.0
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
