@@ -188,3 +188,21 @@ def assert_close(got, want, atol=2e-3, rtol=1e-2, what=""):
 def banner(msg):
     """Names the case on stdout before any GPU work, flushed."""
     print(f"\n[gpu-case] {msg}", flush=True)
+
+
+def pool_token_major(pool, layer, n_layer, max_blocks, n_kv, bt, d, q8):
+    """One layer of a device pool in the reference's token-major paged
+    layout (key_cache[phys][kv_dim], text/generator/detail.hpp:2984-3005):
+    uint16 halves for f16 pools, BLOCK_Q8_0 rows for q8_0 pools (whose
+    regions hold values [bt][d] then scales [bt][d/32])."""
+    lb = pool.numel() // n_layer
+    raw = pool[layer * lb:(layer + 1) * lb].cpu().numpy().reshape(max_blocks, n_kv, -1)
+    if not q8:
+        h = raw.view(np.uint16).reshape(max_blocks, n_kv, bt, d)
+        return np.ascontiguousarray(h.transpose(0, 2, 1, 3)).reshape(max_blocks * bt, n_kv * d)
+    qs = raw[:, :, :bt * d].view(np.int8).reshape(max_blocks, n_kv, bt, d // 32, 32)
+    ds = raw[:, :, bt * d:].view(np.uint16).reshape(max_blocks, n_kv, bt, d // 32)
+    out = np.empty((max_blocks, bt, n_kv, d // 32), oracle.BLOCK_Q8_0)
+    out["qs"] = qs.transpose(0, 2, 1, 3, 4)
+    out["d"] = ds.transpose(0, 2, 1, 3)
+    return out.reshape(max_blocks * bt, n_kv * d // 32)
