@@ -89,8 +89,11 @@ def main():
                     help="with no --config: measure config 3 only (no 'configs' object)")
     ap.add_argument("--cpu-budget", type=float, default=10.0,
                     help="seconds of CPU-baseline work for the headline config")
+    ap.add_argument("--kernel-split", action="store_true",
+                    help="decode configs: add per-kernel durations of one eager step from "
+                         "torch.profiler (a diagnostic, not the roofline basis)")
     ap.add_argument("--no-kernel-split", action="store_true",
-                    help="skip the per-kernel durations from torch.profiler")
+                    help="accepted for older command lines; the split is off by default")
     ap.add_argument("--separate-append", action="store_true",
                     help="append with emelk_kv_append, then emelk_attn_decode (two launches per "
                          "layer) instead of emelk_attn_decode_append")
@@ -309,7 +312,7 @@ def kernel_split(args, torch, fn, names):
     eager call of fn, from torch.profiler's device trace (outside the timed
     region).  Lets the line report the dominant kernel apart from its
     helpers (e.g. decode_kernel vs combine_kernel)."""
-    if args.no_kernel_split:
+    if args.no_kernel_split or not args.kernel_split:
         return None
     try:
         from torch.profiler import ProfilerActivity, profile
@@ -611,7 +614,6 @@ def decode_run(args, torch, emelk, dev):
               if args.config == "llama3-8b-b64-ctx8k" else
               f"KV-read HBM GB/s (% of peak) + decode steps/s, {args.config}")
     traffic = None if args.separate_append else PMC_TRAFFIC_BYTES.get(args.config)
-    dk = (split or {}).get("decode_kernel")
     result = {
         "metric": metric,
         "value": round(kv_gbs, 2),
@@ -639,21 +641,16 @@ def decode_run(args, torch, emelk, dev):
                      "traffic_source": (f"profiles/decode_kernel_{args.config}.md (rocprofv3 "
                                         "--pmc FETCH_SIZE / WRITE_SIZE of an earlier run of this "
                                         "workload, copy-calibrated)") if traffic else None,
-                     "kernel": (("decode_kernel + combine_kernel (HIP events per layer call)"
+                     "kernel": (("decode_kernel + combine_kernel"
                                  if args.separate_append else
-                                 "decode_kernel with the fused append + combine_kernel (HIP events "
-                                 "per layer call)") +
+                                 "decode_kernel with the fused append + combine_kernel") +
                                 (", emelk_attn_decode_contiguous (no block table)"
                                  if contiguous else "")),
                      "bytes_per_launch": kernel_bytes, "avg_launch_ms": round(attn_avg_ms, 4),
-                     "timing": timing_basis,
-                     "decode_kernel_only": ({
-                         "avg_launch_ms": dk["avg_ms"],
-                         "achieved": round(kernel_bytes / (dk["avg_ms"] * 1e-3) / 1e9, 2),
-                         "frac": round(kernel_bytes / (dk["avg_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS,
-                                       4),
-                         "source": "torch.profiler device trace of one eager step"}
-                         if dk else None)},
+                     "timing": timing_basis},
+        "kernel_split": ({"source": "torch.profiler device trace of one eager step "
+                                    "(diagnostic; not the roofline basis)", **split}
+                         if split else None),
         "cpu_baseline": cpu,
         "parity_full_size": parity,
     }

@@ -108,7 +108,17 @@ struct decode_params {
   // plan's split size in tiles bounds the balanced one.
   int32_t balanced;
   int32_t host_tiles;
+  int32_t bt_shift;  // log2(block_tokens) when a power of two, else -1
 };
+
+// log2(block_tokens) when it is a power of two, else -1: the tile loops then
+// find a token's page and row by shift and mask instead of a division.
+inline int32_t pow2_shift(int32_t bt) {
+  for (int32_t b = 0; b < 31; ++b) {
+    if ((1 << b) == bt) return b;
+  }
+  return -1;
+}
 
 // Balanced split plan of a batch of n_seq <= 64 sequences, the same in every
 // wave that computes it: lane i holds sequence i's length, its split count
@@ -961,13 +971,25 @@ __global__ __launch_bounds__(WPB * k_wave) void decode_kernel(decode_params P) {
       const int32_t ta = tbase;        // first token of half 0 (multiple of NGW)
       const int32_t tb = tbase + NGW;  // first token of half 1
       const bool hb = tb < end;
-      const uint32_t pa = __builtin_amdgcn_readfirstlane(s_pages[ta / bt - first_page]);
-      const uint32_t pb =
-          hb ? __builtin_amdgcn_readfirstlane(s_pages[tb / bt - first_page]) : pa;
+      // page index and row of both halves (uniform): shift and mask for
+      // power-of-two pages, else a division
+      int32_t ia, ib, rowa, rowb;
+      if (P.bt_shift >= 0) {
+        ia = ta >> P.bt_shift;
+        ib = tb >> P.bt_shift;
+        rowa = ta & (bt - 1);
+        rowb = tb & (bt - 1);
+      } else {
+        ia = ta / bt;
+        ib = tb / bt;
+        rowa = ta - ia * bt;
+        rowb = tb - ib * bt;
+      }
+      const uint32_t pa = __builtin_amdgcn_readfirstlane(s_pages[ia - first_page]);
+      const uint32_t pb = hb ? __builtin_amdgcn_readfirstlane(s_pages[ib - first_page]) : pa;
       const bool va = pa != 0xFFFFFFFFu;
       const bool vb = pb != 0xFFFFFFFFu && hb;
-      const int32_t rowa = ta % bt;
-      const int32_t rowb = hb ? tb % bt : rowa;
+      rowb = hb ? rowb : rowa;
       ok0 = va && ta + grp < end;
       ok1 = vb && tb + grp < end;
       const uint64_t ra = static_cast<uint64_t>(va ? pa : 0u) * page_bytes;
@@ -1482,6 +1504,7 @@ emel_error_type decode_rows(const pool_layout &L, const void *k_pool, const void
   P.rows = n_q;
   P.balanced = 0;
   P.host_tiles = 0;
+  P.bt_shift = pow2_shift(L.block_tokens);
   const dim3 grid(1, L.n_head_kv / waves_per_block(L.n_head_kv), static_cast<uint32_t>(n_rows));
   if (!dispatch_decode(L, P, grid, st)) return EMELK_ERR_INVALID_REQUEST;
   return hipGetLastError() == hipSuccess ? EMELK_ERR_NONE : EMELK_ERR_BACKEND;
@@ -1577,6 +1600,7 @@ emel_error_type decode_impl(const emelk_kv_geometry *g, const void *k_pool, cons
   const int32_t tile = 2 * (emelk::k_wave / (L.head_dim / 16));
   P.balanced = plan.max_splits > 1 && n_seq > 1 && n_seq <= emelk::k_wave ? 1 : 0;
   P.host_tiles = plan.tokens_per_split / tile;
+  P.bt_shift = emelk::pow2_shift(L.block_tokens);
   P.k_wr = static_cast<uint8_t *>(const_cast<void *>(k_pool));
   P.v_wr = static_cast<uint8_t *>(const_cast<void *>(v_pool));
   const uint64_t acc_floats = static_cast<uint64_t>(n_seq) * L.n_head * plan.max_splits * L.head_dim;
