@@ -72,3 +72,22 @@ def test_decode_shape_sweep(device, case):
         mag[s_] = oracle.attention_f64(qr[s_], k, np.abs(v), sc.n_head, n_kv, D, n, scale)
     assert_close(got, sc.ideal_decode(0, q), atol=2e-3 + 2.0 ** -10 * mag,
                  what="gpu vs fp64 ideal")
+
+
+F16_OUTLIER_CASES = [c for c in _cases(n=40, seed=77) if c[4] == emelk.KV_F16][:6]
+
+
+@pytest.mark.parametrize("case", F16_OUTLIER_CASES,
+                         ids=[f"f16_outliers{i}" for i in range(len(F16_OUTLIER_CASES))])
+def test_decode_f16_with_outliers_strict_bar(device, case):
+    # f16 pools with 1% of K/V values scaled x20, the q8_0 cases' data: the
+    # fp16 rounding of P that both routes do then weighs most, and the GPU
+    # must still stay within the plain bar of the reference route.
+    D, n_kv, group, bt, kv_type, lens, pool_byte, seed = case
+    print(f"\n[gpu-case] f16 outlier decode D={D} n_kv={n_kv} G={group} bt={bt} "
+          f"n_seq={len(lens)} max_len={max(lens)}", flush=True)
+    sc = Scenario(n_layer=1, n_head=n_kv * group, n_kv=n_kv, head_dim=D, block_tokens=bt, lens=lens,
+                  seed=seed, kv_type=kv_type, pool_byte=pool_byte, outlier_frac=0.01)
+    q = np.random.default_rng(seed + 1).standard_normal((sc.n_seq, sc.n_head * D)).astype(np.float32)
+    got = sc.gpu_decode(0, q)
+    assert_close(got, sc.oracle_decode(0, q), what="gpu vs reference route")
