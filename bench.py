@@ -248,17 +248,22 @@ def timed_blocks(torch, stream, launch, reps, prime=None):
 
 
 def graph_event_ms(torch, graph, stream, reps):
-    """HIP event time (ms) per replay of a captured graph, replayed `reps`
-    times back to back between one event pair on `stream` (no host gap can
-    fall between the graph's kernels)."""
+    """(HIP event ms, host ms) per replay of a captured graph, replayed
+    `reps` times back to back: one event pair on `stream` around the
+    replays (no host gap can fall between the graph's kernels), and the host
+    clock around the same replays with a synchronisation on either side, so
+    the event figure never exceeds the host one."""
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
     with torch.cuda.stream(stream):
         e0.record(stream)
         for _ in range(reps):
             graph.replay()
         e1.record(stream)
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / reps
+    host = 1e3 * (time.perf_counter() - t0) / reps
+    return e0.elapsed_time(e1) / reps, host
 
 
 def parity_failures(obj, path=""):
@@ -490,14 +495,9 @@ def decode_run(args, torch, emelk, dev):
         torch.cuda.current_stream().wait_stream(side)
         for _ in range(args.warmup):
             graph.replay()
-        torch.cuda.synchronize()
-        t_start = time.perf_counter()
-        for _ in range(K):
-            graph.replay()
-        torch.cuda.synchronize()
-        graph_ms = 1e3 * (time.perf_counter() - t_start) / K
+        ev_ms, graph_ms = graph_event_ms(torch, graph, side, K)
         if not args.separate_append:
-            attn_avg_ms = graph_event_ms(torch, graph, side, K) / L
+            attn_avg_ms = ev_ms / L
     if attn_avg_ms is None:
         # eager or --separate-append: one HIP event pair around the L
         # back-to-back decode calls of a step after a GPU head start (the
@@ -770,7 +770,7 @@ def prefill_evict(args, torch, emelk, dev):
         g_step.replay()
     torch.cuda.synchronize()
     ms_step = 1e3 * (time.perf_counter() - t0) / K
-    attn_ms = graph_event_ms(torch, g_attn, side, K) / L
+    attn_ms = graph_event_ms(torch, g_attn, side, K)[0] / L
     # bytes the kernel must move per launch: the unique K/V of the layer
     # (prefix + chunk, every KV head), the fp32 queries and the fp32 output
     prefill_bytes = (B * HK * (P0 + NQ) * (page_bytes // (HK * BT)) * 2
