@@ -91,10 +91,12 @@ struct prefill_stage<KI, VI, true> {
 // Returns (hi, lo).  K is staged as both planes: the scores stay exact, since
 // a rounding of K moves a score by up to 2^-11 of sum |q k|, which the
 // softmax amplifies past the 2e-3 bar on data with x20 outliers.  V is staged
-// as hi alone: one rounding of each value (<= 2^-11 relative) enters the
-// output linearly, as the fp16 rounding of P does, at most 2^-11 of
-// sum_p p |v|; it halves the P.V MFMAs and the V^T LDS reads of q8_0 pools
-// (Llama-3-8B chunk shape: 515 vs 610 us per launch).
+// as both planes too, and P as an fp16 hi + lo pair: the P.V MFMAs take
+// P_hi V_hi + P_hi V_lo + P_lo V_hi.  With one fp16 rounding of V (hi alone)
+// and of P, the GPU's own rounding added to the reference route's rounding
+// of its probabilities and went past the bar on x20-outlier data (1.04 of
+// it on a seeded sweep); with both carried this far the GPU's distance to
+// the reference is the reference's own (0.46 of the bar on the same cases).
 __device__ __forceinline__ uint2_v q8_pair_to_f16x2(uint32_t bytes2, half2_t d2) {
   const uint32_t u = bytes2 ^ 0x8080u;
   const half2_t q = as_half2(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) -
@@ -151,7 +153,9 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
   constexpr int PL = Q8 ? 2 : 1;
   __shared__ half_t s_k[2][PL][KT][KROW];
   constexpr int VR = 2;  // V double buffer
-  __shared__ half_t s_vt[VR][D][VROW];
+  // q8_0: V^T as a hi and a lo plane as well (their sum is exact), so P.V
+  // sees the dequantized values unrounded
+  __shared__ half_t s_vt[VR][PL][D][VROW];
   __shared__ float s_row[WAVES][32];
   __shared__ uint16_t s_ptab[k_max_seq_pages];
 
@@ -593,13 +597,13 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
         // row: chosen by the permute selector, not by selecting data
         const uint32_t sel_first = odd_first ? 0x07060302u : 0x05040100u;
         const uint32_t sel_second = odd_first ? 0x05040100u : 0x07060302u;
-        auto put = [&](uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) {
+        auto put = [&](int pl, uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) {
           const uint2 first{__builtin_amdgcn_perm(w1, w0, sel_first),
                             __builtin_amdgcn_perm(w3, w2, sel_first)};
           const uint2 second{__builtin_amdgcn_perm(w1, w0, sel_second),
                              __builtin_amdgcn_perm(w3, w2, sel_second)};
-          *reinterpret_cast<uint2 *>(&s_vt[vbuf][r0][slot]) = first;
-          *reinterpret_cast<uint2 *>(&s_vt[vbuf][r0 ^ 1][slot]) = second;
+          *reinterpret_cast<uint2 *>(&s_vt[vbuf][pl][r0][slot]) = first;
+          *reinterpret_cast<uint2 *>(&s_vt[vbuf][pl][r0 ^ 1][slot]) = second;
         };
         if constexpr (Q8) {
           uint2_v w[4];
@@ -607,9 +611,10 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
           for (int e = 0; e < 4; ++e) {
             w[e] = q8_pair_to_f16x2(R.rv[i][e] & 0xFFFFu, as_half2((R.rv[i][e] >> 16) * 0x10001u));
           }
-          put(w[0].x, w[1].x, w[2].x, w[3].x);  // the hi plane: fp16(q * d)
+          put(0, w[0].x, w[1].x, w[2].x, w[3].x);  // hi: fp16(q * d)
+          put(PL - 1, w[0].y, w[1].y, w[2].y, w[3].y);  // lo: q * d - hi, exact
         } else {
-          put(R.rv[i][0], R.rv[i][1], R.rv[i][2], R.rv[i][3]);
+          put(0, R.rv[i][0], R.rv[i][1], R.rv[i][2], R.rv[i][3]);
         }
       }
     }
@@ -780,29 +785,42 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
 #pragma unroll
       for (int st = 0; st < 2; ++st) {
         half8_v pa;
+        [[maybe_unused]] half8_v pl;  // q8_0: P - fp16(P), so hi + lo carries P to about 2^-22
 #pragma unroll
-        for (int i = 0; i < 8; ++i) pa[i] = static_cast<half_t>(s[j][8 * st + i]);
+        for (int i = 0; i < 8; ++i) {
+          pa[i] = static_cast<half_t>(s[j][8 * st + i]);
+          if constexpr (Q8) pl[i] = static_cast<half_t>(s[j][8 * st + i] - static_cast<float>(pa[i]));
+        }
 #pragma unroll
         for (int c = 0; c < DCH; ++c) {
           const half8_v b = *reinterpret_cast<const half8_v *>(
-              &s_vt[buf][32 * c + l32][j * k_sub + 16 * st + 8 * h]);
+              &s_vt[buf][0][32 * c + l32][j * k_sub + 16 * st + 8 * h]);
           o[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, b, o[c], 0, 0, 0);
+          if constexpr (Q8) {
+            // P_hi V_lo + P_lo V_hi; P_lo V_lo (about 2^-22 of P V) is left out
+            const half8_v bl = *reinterpret_cast<const half8_v *>(
+                &s_vt[buf][PL - 1][32 * c + l32][j * k_sub + 16 * st + 8 * h]);
+            o[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, bl, o[c], 0, 0, 0);
+            o[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pl, b, o[c], 0, 0, 0);
+          }
         }
       }
     }
     {
       // the V operand reads run four MFMAs ahead (measured 2% faster than
       // the compiler's own order at the Llama-3-8B chunk shape)
+      // (q8_0: per operand pair, 2 reads and 3 MFMAs)
       constexpr int NPV = NS * 2 * DCH;
       constexpr int LAP = 4;
-      __builtin_amdgcn_sched_group_barrier(0x100, LAP, 1);
+      constexpr int RD = Q8 ? 2 : 1, MF = Q8 ? 3 : 1;
+      __builtin_amdgcn_sched_group_barrier(0x100, LAP * RD, 1);
 #pragma unroll
       for (int k = 0; k < NPV - LAP; ++k) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+        __builtin_amdgcn_sched_group_barrier(0x008, MF, 1);
+        __builtin_amdgcn_sched_group_barrier(0x100, RD, 1);
       }
 #pragma unroll
-      for (int k = 0; k < LAP; ++k) __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+      for (int k = 0; k < LAP; ++k) __builtin_amdgcn_sched_group_barrier(0x008, MF, 1);
     }
   };
 
@@ -950,7 +968,7 @@ __global__ __launch_bounds__(G_WG * RB * k_wave) void prefill_kernel(prefill_par
 #pragma unroll
     for (int c = 0; c < OT16; ++c) {
       const half8_v b =
-          *reinterpret_cast<const half8_v *>(&s_vt[buf][16 * c + c16][8 * g16]);
+          *reinterpret_cast<const half8_v *>(&s_vt[buf][0][16 * c + c16][8 * g16]);
       o16[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, b, o16[c], 0, 0, 0);
     }
   };

@@ -339,8 +339,8 @@ emel_error_type emelk_attn_decode_noalloc(const emelk_kv_geometry *g, void *k_po
  * row of sequence s attend to nothing: its rows are written as zeros, on
  * every route.  head_dim 64 and 128 run on MFMA,
  * f16 and q8_0 pools alike (q8_0 K values enter the score MFMAs exactly, as
- * two fp16 parts, values of magnitude 65520 or more excepted; q8_0 V values
- * as fp16(q * d), one rounding), and so do
+ * two fp16 parts, values of magnitude 65520 or more excepted, and q8_0 V
+ * values the same way in the P.V MFMAs, with P as two fp16 parts), and so do
  * head_dim 256 and, on f16 pools, 512.  q8_0 at head_dim 512 runs row by
  * row through the decode kernel (n_seq * n_q <= 65535, and a row's
  * context, table_stride * block_tokens tokens at most, must fit 1022
