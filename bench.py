@@ -51,11 +51,11 @@ PMC_TRAFFIC_BYTES = {  # workload -> bytes; source: profiles/<kernel>_<workload>
     "llama3-8b-b64-ctx8k": 2157021798,
     "llama3-8b-q8_0-b32-ctx16k": 1150230950,
     "llama3-8b-prefill512-evict25": 287648388,
-    "llama3-8b-q8_0-prefill512-evict25": 290576846,
+    "llama3-8b-q8_0-prefill512-evict25": 292694400,
     "llama3.2-1b-b16-ctx1k-4k": 96741730,
     "qwen3-0.6b-b1-ctx512": 2627852,
     "gemma4-d256-prefill512-evict25": 105300848,
-    "gemma4-d256-q8_0-prefill512-evict25": 87748528,
+    "gemma4-d256-q8_0-prefill512-evict25": 87734776,
     "gemma4-d512-prefill512-evict25": 285765904,
 }
 
